@@ -1,0 +1,383 @@
+// Fused attention: softmax(Q_h K_h^T * scale + mask) V_h over packed
+// [B, T, H*d] rows, the semantics of DmlOps.MultiheadAttention
+// (Dml/DmlOps.cs:480-520; a ruled-out score gets -10000 added, :483).
+//
+// flash_attn_kernel (bf16 / f16, d = 64 or 128): a workgroup of 4 waves takes
+// 128 queries of one (batch, head); each wave owns 32 queries. Scores are
+// computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16: lane l then holds
+// column l % 32 of S^T, i.e. one query, so the running max, the rescale of
+// the output and the row sum are per-lane registers and one exchange with
+// lane l ^ 32. The output is accumulated transposed, O^T += V^T P^T, with P^T
+// fed straight from the score registers: the key order inside each 16-key
+// MFMA step is permuted identically on both operands, so V^T is read from
+// LDS in that order and no score ever leaves registers. K and V^T tiles of 64
+// keys are double buffered in LDS (V transposed on its way in), swizzled by
+// 16- and 8-byte granules.
+//
+// attn_generic_kernel: any float type and head size, fp32 arithmetic with
+// expf; the fp32-compute path and the reference for odd shapes.
+
+#include "k_common.h"
+
+namespace ndx {
+
+template <typename T>
+struct AMfma;
+template <>
+struct AMfma<__bf16> {
+  typedef bf16x8 V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct AMfma<_Float16> {
+  typedef f16x8 V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ const T* seg_row(const AttnSeg& s, int64_t b, int64_t r) {
+  if (r < s.rows0) return (const T*)s.ptr[0] + b * s.batch[0] + r * s.ld[0];
+  return (const T*)s.ptr[1] + b * s.batch[1] + (r - s.rows0) * s.ld[1];
+}
+
+__device__ __forceinline__ void* out_row(const AttnArgs& a, int64_t b, int64_t r, int esize) {
+  if (r < a.out_rows0) return (char*)a.out[0] + (b * a.out_batch[0] + r * a.out_ld[0]) * esize;
+  return (char*)a.out[1] + (b * a.out_batch[1] + (r - a.out_rows0) * a.out_ld[1]) * esize;
+}
+
+// Decodes a workgroup id into (query block, head, batch), keeping each XCD on
+// a contiguous run so the query blocks of one head share that XCD's L2.
+__device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H, int B, int& qb, int& h, int& b) {
+  const int per = grid / 8;
+  pid = (pid % 8) * per + pid / 8;
+  if (pid >= qblocks * H * B) return false;
+  qb = pid % qblocks;
+  int r = pid / qblocks;
+  h = r % H;
+  b = r / H;
+  return true;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
+  typedef typename AMfma<T>::V V;
+  constexpr int BQ = 128, BKEY = 64;
+  constexpr int KCH = D / 8;                      // 16-byte chunks per key row
+  constexpr int KMASK = (KCH < 16 ? KCH : 16) - 1;
+  constexpr int K_PER = BKEY * KCH / 256;         // K chunks per thread
+  constexpr int V_TASKS = (BKEY / 4) * (D / 8);   // (4-key group, 8-d chunk) tasks
+  constexpr int DT = D / 32;                      // output tiles along d
+  __shared__ __attribute__((aligned(16))) T Ks[2][BKEY * D];
+  __shared__ __attribute__((aligned(16))) T Vt[2][D * BKEY];
+
+  int qb, head, b;
+  if (!attn_tile(blockIdx.x, grid, (a.T + BQ - 1) / BQ, a.H, a.B, qb, head, b)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lq = lane & 31, lh = lane >> 5;
+  const int q0 = qb * BQ + wave * 32;
+  const int qi = q0 + lq;
+  const int64_t col0 = int64_t(head) * D;
+
+  // Q^T fragments, resident for the whole key loop.
+  V qf[D / 16];
+  {
+    const T* qrow = qi < a.T ? seg_row<T>(a.q, b, qi) + col0 : nullptr;
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) {
+      if (qrow)
+        qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
+      else
+        for (int e = 0; e < 8; e++) qf[s][e] = (T)0.f;
+    }
+  }
+
+  uint4 rk[K_PER];
+  uint4 rv[4];
+  const int vtask = tid;
+  const int vkg = vtask / (D / 8), vdc = vtask % (D / 8);
+  auto load_kv = [&](int kb) {
+    const int key0 = kb * BKEY;
+#pragma unroll
+    for (int i = 0; i < K_PER; i++) {
+      int id = tid + i * 256;
+      int key = id / KCH, c = id % KCH;
+      int gk = key0 + key;
+      rk[i] = gk < a.S ? *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8) : make_uint4(0, 0, 0, 0);
+    }
+    if (vtask < V_TASKS) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        int gk = key0 + vkg * 4 + e;
+        rv[e] = gk < a.S ? *(const uint4*)(seg_row<T>(a.v, b, gk) + col0 + vdc * 8) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < K_PER; i++) {
+      int id = tid + i * 256;
+      int key = id / KCH, c = id % KCH;
+      *(uint4*)&Ks[buf][key * D + ((c ^ (key & KMASK)) << 3)] = rk[i];
+    }
+    if (vtask < V_TASKS) {
+      const uint16_t* v0 = (const uint16_t*)&rv[0];
+      const uint16_t* v1 = (const uint16_t*)&rv[1];
+      const uint16_t* v2 = (const uint16_t*)&rv[2];
+      const uint16_t* v3 = (const uint16_t*)&rv[3];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        int d = vdc * 8 + e;
+        uint2 g;
+        g.x = uint32_t(v0[e]) | (uint32_t(v1[e]) << 16);
+        g.y = uint32_t(v2[e]) | (uint32_t(v3[e]) << 16);
+        *(uint2*)&Vt[buf][d * BKEY + ((vkg ^ (d & 15)) << 2)] = g;
+      }
+    }
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; t++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[t][r] = 0.f;
+  float m_run = -INFINITY, l_part = 0.f;
+  const float sl = a.scale * kLog2e;
+  const float mask_add = -10000.0f * kLog2e;
+  int key_len = a.S;
+  if (a.mask_kind == NDX_MASK_KEY_LENGTH) key_len = a.mask[0];
+
+  const int KB = (a.S + BKEY - 1) / BKEY;
+  load_kv(0);
+  store_kv(0);
+  __syncthreads();
+  for (int kb = 0; kb < KB; kb++) {
+    const int cur = kb & 1;
+    if (kb + 1 < KB) load_kv(kb + 1);
+
+    // S^T for 64 keys: two 32-key tiles.
+    f32x16 sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) sacc[t][r] = 0.f;
+      const int key = t * 32 + lq;
+#pragma unroll
+      for (int s = 0; s < D / 16; s++) {
+        const int c = 2 * s + lh;
+        V kf = *(const V*)&Ks[cur][key * D + ((c ^ (key & KMASK)) << 3)];
+        sacc[t] = AMfma<T>::mma(kf, qf[s], sacc[t]);
+      }
+    }
+    // Scale, mask, running max.
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int key = kb * BKEY + t * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        float x = sacc[t][r] * sl;
+        if (key >= a.S) {
+          x = -INFINITY;
+        } else if (a.mask_kind == NDX_MASK_KEY_LENGTH) {
+          if (key >= key_len) x += mask_add;
+        } else if (a.mask_kind == NDX_MASK_BOOLEAN && qi < a.T) {
+          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qi) * a.mask_stride[2] +
+                             int64_t(key) * a.mask_stride[3];
+          if (a.mask[mi] == 0) x += mask_add;
+        }
+        sacc[t][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float p = exp2f(sacc[t][r] - m_new);
+        sacc[t][r] = p;
+        psum += p;
+      }
+    l_part = l_part * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+
+    // O^T += V^T P^T over four 16-key steps.
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      V pb;
+#pragma unroll
+      for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
+#pragma unroll
+      for (int t = 0; t < DT; t++) {
+        const int d = t * 32 + lq;
+        const int g1 = 4 * u + lh, g2 = 4 * u + 2 + lh;
+        uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
+        uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
+        V vf;
+        uint4 packed = make_uint4(x1.x, x1.y, x2.x, x2.y);
+        vf = *(const V*)&packed;
+        o[t] = AMfma<T>::mma(vf, pb, o[t]);
+      }
+    }
+    if (kb + 1 < KB) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < a.T) {
+    T* orow = (T*)out_row(a, b, qi, sizeof(T)) + col0;
+#pragma unroll
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = t * 32 + 8 * g + 4 * lh;
+        T v4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v4[e] = (T)(o[t][g * 4 + e] * inv);
+        *(uint2*)(orow + d) = *(const uint2*)v4;
+      }
+  }
+}
+
+// ---- generic ----------------------------------------------------------------
+
+// 16 queries of one (batch, head) per workgroup, 4 per wave; 64-key tiles
+// of K and V in LDS; lane j scores key j, lanes split d for the output.
+constexpr int GQ = 16, GK = 64, GDMAX = 128;
+
+__device__ __forceinline__ const char* seg_row_bytes(const AttnSeg& s, int64_t b, int64_t r, int esize) {
+  if (r < s.rows0) return (const char*)s.ptr[0] + (b * s.batch[0] + r * s.ld[0]) * esize;
+  return (const char*)s.ptr[1] + (b * s.batch[1] + (r - s.rows0) * s.ld[1]) * esize;
+}
+
+__global__ __launch_bounds__(256) void attn_generic_kernel(AttnArgs a) {
+  extern __shared__ float sm[];
+  const int D = a.d, DV = a.dv;
+  float* Qs = sm;                  // [GQ][D]
+  float* Ks = Qs + GQ * D;         // [GK][D + 1]
+  float* Vs = Ks + GK * (D + 1);   // [GK][DV]
+  float* Ps = Vs + GK * DV;        // [GQ][GK]
+  const int esize = dtype_size(a.dtype);
+  const int qb = blockIdx.x, head = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < GQ * D; i += 256) {
+    int q = qb * GQ + i / D;
+    Qs[i] = q < a.T ? load_f(seg_row_bytes(a.q, b, q, esize), a.dtype, int64_t(head) * D + i % D) : 0.f;
+  }
+  float m_run[4], l_run[4], acc[4][GDMAX / 64];
+  for (int q = 0; q < 4; q++) {
+    m_run[q] = -INFINITY;
+    l_run[q] = 0.f;
+    for (int e = 0; e < GDMAX / 64; e++) acc[q][e] = 0.f;
+  }
+  int key_len = a.mask_kind == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
+  for (int k0 = 0; k0 < a.S; k0 += GK) {
+    __syncthreads();
+    for (int i = tid; i < GK * D; i += 256) {
+      int key = k0 + i / D;
+      Ks[(i / D) * (D + 1) + i % D] =
+          key < a.S ? load_f(seg_row_bytes(a.k, b, key, esize), a.dtype, int64_t(head) * D + i % D) : 0.f;
+    }
+    for (int i = tid; i < GK * DV; i += 256) {
+      int key = k0 + i / DV;
+      Vs[i] = key < a.S ? load_f(seg_row_bytes(a.v, b, key, esize), a.dtype, int64_t(head) * DV + i % DV) : 0.f;
+    }
+    __syncthreads();
+    for (int q = 0; q < 4; q++) {
+      const int ql = wave * 4 + q, qi = qb * GQ + ql;
+      const int key = k0 + lane;
+      float x = -INFINITY;
+      if (key < a.S) {
+        float dot = 0.f;
+        for (int d = 0; d < D; d++) dot += Qs[ql * D + d] * Ks[lane * (D + 1) + d];
+        x = dot * a.scale;
+        if (a.mask_kind == NDX_MASK_KEY_LENGTH && key >= key_len) x += -10000.0f;
+        if (a.mask_kind == NDX_MASK_BOOLEAN && qi < a.T) {
+          int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qi) * a.mask_stride[2] +
+                       int64_t(key) * a.mask_stride[3];
+          if (a.mask[mi] == 0) x += -10000.0f;
+        }
+      }
+      const float m_new = fmaxf(m_run[q], wave_max(x));
+      const float alpha = expf(m_run[q] - m_new);
+      const float p = key < a.S ? expf(x - m_new) : 0.f;
+      l_run[q] = l_run[q] * alpha + wave_sum(p);
+      m_run[q] = m_new;
+      Ps[ql * GK + lane] = p;
+      for (int e = 0; e < GDMAX / 64; e++) acc[q][e] *= alpha;
+    }
+    __syncthreads();
+    for (int q = 0; q < 4; q++) {
+      const int ql = wave * 4 + q;
+      for (int e = 0; e < GDMAX / 64; e++) {
+        int d = lane + e * 64;
+        if (d >= DV) break;
+        float s = 0.f;
+        for (int j = 0; j < GK; j++) s += Ps[ql * GK + j] * Vs[j * DV + d];
+        acc[q][e] += s;
+      }
+    }
+  }
+  for (int q = 0; q < 4; q++) {
+    const int qi = qb * GQ + wave * 4 + q;
+    if (qi >= a.T) continue;
+    char* orow = (char*)out_row(a, b, qi, esize);
+    for (int e = 0; e < GDMAX / 64; e++) {
+      int d = lane + e * 64;
+      if (d >= DV) break;
+      store_f(orow, a.dtype, int64_t(head) * DV + d, acc[q][e] / l_run[q]);
+    }
+  }
+}
+
+static bool rows_aligned(const AttnSeg& s, int esize) {
+  for (int p = 0; p < 2; p++) {
+    if ((uintptr_t)s.ptr[p] % 16) return false;
+    if ((s.ld[p] * esize) % 16 || (s.batch[p] * esize) % 16) return false;
+  }
+  return true;
+}
+
+void launch_attention(const AttnArgs& a, hipStream_t s) {
+  if (a.T == 0 || a.B == 0) return;
+  const bool mfma = (a.dtype == NDX_BF16 || a.dtype == NDX_F16) && a.d == a.dv && (a.d == 128 || a.d == 64) &&
+                    rows_aligned(a.q, 2) && rows_aligned(a.k, 2) && rows_aligned(a.v, 2) &&
+                    (uintptr_t)a.out[0] % 16 == 0 && (uintptr_t)a.out[1] % 16 == 0;
+  if (mfma) {
+    int qblocks = (a.T + 127) / 128;
+    int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
+    if (a.dtype == NDX_BF16) {
+      if (a.d == 128) hipLaunchKernelGGL((flash_attn_kernel<__bf16, 128>), dim3(grid), dim3(256), 0, s, a, grid);
+      else hipLaunchKernelGGL((flash_attn_kernel<__bf16, 64>), dim3(grid), dim3(256), 0, s, a, grid);
+    } else {
+      if (a.d == 128) hipLaunchKernelGGL((flash_attn_kernel<_Float16, 128>), dim3(grid), dim3(256), 0, s, a, grid);
+      else hipLaunchKernelGGL((flash_attn_kernel<_Float16, 64>), dim3(grid), dim3(256), 0, s, a, grid);
+    }
+    return;
+  }
+  size_t lds = (size_t(GQ) * a.d + size_t(GK) * (a.d + 1) + size_t(GK) * a.dv + size_t(GQ) * GK) * sizeof(float);
+  static bool raised = false;
+  if (!raised) {
+    hip_check(hipFuncSetAttribute((const void*)attn_generic_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024),
+              "attention LDS limit");
+    raised = true;
+  }
+  dim3 grid((a.T + GQ - 1) / GQ, a.H, a.B);
+  hipLaunchKernelGGL(attn_generic_kernel, grid, dim3(256), lds, s, a);
+}
+
+}  // namespace ndx

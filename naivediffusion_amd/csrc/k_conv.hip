@@ -1,0 +1,61 @@
+// 2-D convolution (cross-correlation) over NCHW, the semantics of
+// DmlOps.Convolution (Dml/DmlOps.cs:265-299): filters [Cout, Cin, kh, kw],
+// start padding `pad` on both spatial axes (the end padding only changes the
+// output extent, which the graph computed), bias per output channel, an
+// optional residual added to the output. Filters may be int8 with block
+// scales along Cin*kh*kw (ModelBuilder.Weight, Graph/ModelBuilder.cs:61-64).
+//
+// Direct form: one thread per output element, fp32 accumulation.
+
+#include "k_common.h"
+
+namespace ndx {
+
+__global__ void conv2d_direct_kernel(ConvArgs a, int64_t total) {
+  const int taps = a.Cin * a.kh * a.kw;
+  const int lds = a.qblock ? taps / a.qblock : 0;
+  for (int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; id < total;
+       id += int64_t(gridDim.x) * blockDim.x) {
+    int64_t r = id;
+    const int ox = (int)(r % a.Wo);
+    r /= a.Wo;
+    const int oy = (int)(r % a.Ho);
+    r /= a.Ho;
+    const int co = (int)(r % a.Cout);
+    const int64_t n = r / a.Cout;
+    float acc = 0.f;
+    for (int ci = 0; ci < a.Cin; ci++) {
+      const int64_t xb = (n * a.Cin + ci) * int64_t(a.H) * a.W;
+      for (int ky = 0; ky < a.kh; ky++) {
+        const int iy = oy * a.stride - a.pad + ky;
+        if (iy < 0 || iy >= a.H) continue;
+        for (int kx = 0; kx < a.kw; kx++) {
+          const int ix = ox * a.stride - a.pad + kx;
+          if (ix < 0 || ix >= a.W) continue;
+          const int tap = (ci * a.kh + ky) * a.kw + kx;
+          const int64_t wi = int64_t(co) * taps + tap;
+          float w;
+          if (a.w_dtype == NDX_I8) {
+            float sc = a.s_dtype == NDX_F16 ? (float)((const _Float16*)a.scales)[int64_t(co) * lds + tap / a.qblock]
+                                            : ((const float*)a.scales)[int64_t(co) * lds + tap / a.qblock];
+            w = float(((const int8_t*)a.w)[wi]) * sc;
+          } else {
+            w = load_f(a.w, a.w_dtype, wi);
+          }
+          acc += load_f(a.x, a.x_dtype, xb + int64_t(iy) * a.W + ix) * w;
+        }
+      }
+    }
+    if (a.bias) acc += load_f(a.bias, a.bias_dtype, co);
+    if (a.resid) acc += load_f(a.resid, a.y_dtype, id);
+    store_f(a.y, a.y_dtype, id, acc);
+  }
+}
+
+void launch_conv2d(const ConvArgs& a, hipStream_t s) {
+  int64_t total = int64_t(a.N) * a.Cout * a.Ho * a.Wo;
+  int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536 * 4);
+  hipLaunchKernelGGL(conv2d_direct_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, s, a, total);
+}
+
+}  // namespace ndx

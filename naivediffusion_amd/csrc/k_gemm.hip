@@ -1,0 +1,576 @@
+// The linear layer's GEMM for gfx950: y[M, N] = x[M, K] * W[N, K]^T with
+// fused epilogues (bias, GELU-tanh / GELU / SiLU, gated residual).
+//
+// Both operands are K-contiguous rows (torch's [out, in] weight order, the
+// layout Layers.Linear feeds DirectML, Graph/Layers.cs:131-160), so A and B
+// tiles load the same way: 16-byte chunks of 8 elements, staged through LDS
+// in a double buffer, each 64-element K row of the tile XOR-swizzled by 16-
+// byte chunk so the MFMA fragment reads are bank-conflict free.
+//
+// Kernels:
+//  - gemm_mfma_kernel: bf16 or f16 activations on v_mfma_f32_32x32x16_{bf16,f16};
+//    weights of the same type or int8 with per-(row, block) scales that are
+//    dequantised in registers on the way into LDS.
+//  - gemm_f32_kernel: fp32 activations on v_mfma_f32_32x32x2_f32; weights of
+//    any float width or int8, widened on the way into LDS.
+//  - gemv_kernel: a handful of rows (the adaLN modulation, the time MLP):
+//    weight-bandwidth bound, one wave per output feature group.
+//  - gemm_generic_kernel: DmlOps.Gemm with arbitrary strides and transposes.
+
+#include "k_common.h"
+
+namespace ndx {
+
+static constexpr int BK = 64;
+
+template <typename T>
+struct MfmaOp;
+template <>
+struct MfmaOp<__bf16> {
+  typedef bf16x8 V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static constexpr int dtype = NDX_BF16;
+};
+template <>
+struct MfmaOp<_Float16> {
+  typedef f16x8 V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static constexpr int dtype = NDX_F16;
+};
+
+// Tile order: workgroup i runs on XCD i % 8, so consecutive ids are
+// re-indexed to give each XCD one contiguous run of tiles, and tiles are
+// walked in groups of 8 tile-rows so neighbours share A rows and W rows in
+// that XCD's L2.
+__device__ __forceinline__ bool tile_of(int pid, int grid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per = grid / 8;
+  pid = (pid % 8) * per + pid / 8;
+  if (pid >= tiles_m * tiles_n) return false;
+  const int G = 8;
+  const int width = G * tiles_n;
+  const int group = pid / width;
+  const int first_m = group * G;
+  const int gsz = min(tiles_m - first_m, G);
+  tm = first_m + (pid % width) % gsz;
+  tn = (pid % width) / gsz;
+  return true;
+}
+
+__device__ __forceinline__ float scale_at(const void* s, int sdt, int64_t i) {
+  return sdt == NDX_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
+}
+
+// The epilogue of one output element (row, col) of batch b.
+__device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t b, int row, int col, float v, float bias,
+                                             float gate) {
+  v += bias;
+  switch (a.epilogue) {
+    case EPI_GELU_TANH: v = gelu_tanh_f(v); break;
+    case EPI_GELU: v = gelu_f(v); break;
+    case EPI_SILU: v = silu_f(v); break;
+    case EPI_GATED_RESIDUAL:
+      v = load_f(a.resid, a.r_dtype, b * a.batch_r + int64_t(row) * a.ldr + col) + gate * round_to(v, a.a_dtype);
+      break;
+    case EPI_RESIDUAL:
+      v = load_f(a.resid, a.r_dtype, b * a.batch_r + int64_t(row) * a.ldr + col) + round_to(v, a.a_dtype);
+      break;
+    default: break;
+  }
+  store_f(a.c, a.c_dtype, b * a.batch_c + int64_t(row) * a.ldc + col, v);
+}
+
+// Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ (r & 7)) << 3); }
+
+template <int BM, int BN, int WM, int WN, typename T, bool W_INT8>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmArgs a, int grid) {
+  typedef typename MfmaOp<T>::V V;
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NT = (BM / WM) * (BN / WN) * 64;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_PER = BM * (BK / 8) / NT;
+  constexpr int B_CHUNK = W_INT8 ? 16 : 8;  // elements per 16-byte global load
+  constexpr int B_PER = BN * (BK / B_CHUNK) / NT;
+  static_assert(A_PER * NT == BM * (BK / 8), "A tile does not split over the threads");
+  static_assert(B_PER * NT == BN * (BK / B_CHUNK), "B tile does not split over the threads");
+
+  __shared__ __attribute__((aligned(16))) T As[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) T Bs[2][BN * BK];
+
+  int tm, tn;
+  if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
+  const int64_t bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  const T* A = (const T*)a.a + bidx * a.batch_a;
+  const char* W = (const char*)a.w + bidx * a.batch_w * (W_INT8 ? 1 : (int)sizeof(T));
+
+  uint4 ra[A_PER];
+  uint4 rb[B_PER];
+  float rs[W_INT8 ? B_PER : 1];
+
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      int id = tid + i * NT;
+      int r = id >> 3, c = id & 7;
+      int gm = m0 + r, gk = k0 + c * 8;
+      if (gm < a.M && gk < a.K)
+        ra[i] = *(const uint4*)(A + int64_t(gm) * a.lda + gk);
+      else
+        ra[i] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      int id = tid + i * NT;
+      int r = id / (BK / B_CHUNK), c = id % (BK / B_CHUNK);
+      int gn = n0 + r, gk = k0 + c * B_CHUNK;
+      if (gn < a.N && gk < a.K) {
+        if (W_INT8) {
+          rb[i] = *(const uint4*)(W + int64_t(gn) * a.ldw + gk);
+          rs[W_INT8 ? i : 0] = scale_at(a.scales, a.s_dtype, int64_t(gn) * a.lds + gk / a.qblock);
+        } else {
+          rb[i] = *(const uint4*)(W + (int64_t(gn) * a.ldw + gk) * (int)sizeof(T));
+        }
+      } else {
+        rb[i] = make_uint4(0, 0, 0, 0);
+        if (W_INT8) rs[W_INT8 ? i : 0] = 0.f;
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      int id = tid + i * NT;
+      int r = id >> 3, c = id & 7;
+      *(uint4*)&As[buf][swz(r, c)] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      int id = tid + i * NT;
+      if (W_INT8) {
+        int r = id / (BK / 16), c = id % (BK / 16);
+        const int8_t* q = (const int8_t*)&rb[i];
+        float s = rs[W_INT8 ? i : 0];
+        V lo, hi;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          lo[e] = (T)(float(q[e]) * s);
+          hi[e] = (T)(float(q[e + 8]) * s);
+        }
+        *(V*)&Bs[buf][swz(r, 2 * c)] = lo;
+        *(V*)&Bs[buf][swz(r, 2 * c + 1)] = hi;
+      } else {
+        int r = id >> 3, c = id & 7;
+        *(uint4*)&Bs[buf][swz(r, c)] = rb[i];
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int KT = (a.K + BK - 1) / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_tile(kt + 1);
+#pragma unroll
+    for (int s = 0; s < BK / 16; s++) {
+      V af[TM], bf[TN];
+      const int c = 2 * s + lhalf;
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, c)];
+#pragma unroll
+      for (int j = 0; j < TN; j++) bf[j] = *(const V*)&Bs[cur][swz(wn * WN + j * 32 + lrow, c)];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Lane l of a 32x32 result holds column l % 32 and rows
+  // 8 * (r / 4) + 4 * (l / 32) + r % 4 for r = 0..15.
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int col = n0 + wn * WN + j * 32 + lrow;
+    if (col >= a.N) continue;
+    const float bias = a.bias ? load_f(a.bias, a.bias_dtype, col) : 0.f;
+    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + col) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        if (row < a.M) epilogue_one(a, bidx, row, col, acc[i][j][r], bias, gate);
+      }
+    }
+  }
+}
+
+// ---- fp32 -------------------------------------------------------------------
+
+static constexpr int BK32 = 32;
+__device__ __forceinline__ int swz32(int r, int c) { return r * BK32 + ((c ^ (r & 7)) << 2); }
+
+// Eight consecutive weights starting at element (row n, column k) widened
+// to fp32 (any float width, or int8 times its block scale).
+__device__ __forceinline__ void load_w8(const GemmArgs& a, const char* W, int n, int k, float* out) {
+  switch (a.w_dtype) {
+    case NDX_F32: {
+      const float4* p = (const float4*)(W + (int64_t(n) * a.ldw + k) * 4);
+      float4 x = p[0], y = p[1];
+      out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+      out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
+      break;
+    }
+    case NDX_BF16: {
+      uint4 v = *(const uint4*)(W + (int64_t(n) * a.ldw + k) * 2);
+      const uint16_t* h = (const uint16_t*)&v;
+      for (int e = 0; e < 8; e++) out[e] = bf16_bits_to_f32(h[e]);
+      break;
+    }
+    case NDX_F16: {
+      uint4 v = *(const uint4*)(W + (int64_t(n) * a.ldw + k) * 2);
+      const _Float16* h = (const _Float16*)&v;
+      for (int e = 0; e < 8; e++) out[e] = (float)h[e];
+      break;
+    }
+    default: {  // int8
+      uint2 v = *(const uint2*)(W + int64_t(n) * a.ldw + k);
+      const int8_t* q = (const int8_t*)&v;
+      float s = scale_at(a.scales, a.s_dtype, int64_t(n) * a.lds + k / a.qblock);
+      for (int e = 0; e < 8; e++) out[e] = float(q[e]) * s;
+      break;
+    }
+  }
+}
+
+// fp32 activations: 128x128 tiles of four 64x64 waves on the fp32 MFMA.
+// Within a 16-wide K step, lane half h feeds k = h*8 + t to MFMA number t,
+// the same permutation for both operands, so eight MFMAs cover the step
+// from one 16-byte-pair LDS read per operand.
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
+  constexpr int BM = 128, BN = 128, WM = 64, WN = 64, TM = 2, TN = 2;
+  __shared__ __attribute__((aligned(16))) float As[2][BM * BK32];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * BK32];
+  int tm, tn;
+  if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
+  const int64_t bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / 2, wn = wave % 2;
+  const float* A = (const float*)a.a + bidx * a.batch_a;
+  const char* W = (const char*)a.w;
+
+  float4 ra[4];
+  float rb[2][8];
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * BK32;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int id = tid + i * 256;
+      int r = id >> 3, c = id & 7;
+      int gm = m0 + r, gk = k0 + c * 4;
+      if (gm < a.M && gk < a.K)
+        ra[i] = *(const float4*)(A + int64_t(gm) * a.lda + gk);
+      else
+        ra[i] = make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      int id = tid + i * 256;
+      int r = id >> 2, c = id & 3;
+      int gn = n0 + r, gk = k0 + c * 8;
+      if (gn < a.N && gk < a.K)
+        load_w8(a, W, gn, gk, rb[i]);
+      else
+        for (int e = 0; e < 8; e++) rb[i][e] = 0.f;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int id = tid + i * 256;
+      int r = id >> 3, c = id & 7;
+      *(float4*)&As[buf][swz32(r, c)] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      int id = tid + i * 256;
+      int r = id >> 2, c = id & 3;
+      *(float4*)&Bs[buf][swz32(r, 2 * c)] = make_float4(rb[i][0], rb[i][1], rb[i][2], rb[i][3]);
+      *(float4*)&Bs[buf][swz32(r, 2 * c + 1)] = make_float4(rb[i][4], rb[i][5], rb[i][6], rb[i][7]);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int KT = (a.K + BK32 - 1) / BK32;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_tile(kt + 1);
+#pragma unroll
+    for (int s = 0; s < BK32 / 16; s++) {
+      float af[TM][8], bf[TN][8];
+      const int c = 4 * s + 2 * lhalf;  // two 4-float chunks: k = s*16 + h*8 + 0..7
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        int r = wm * WM + i * 32 + lrow;
+        float4 x = *(const float4*)&As[cur][swz32(r, c)];
+        float4 y = *(const float4*)&As[cur][swz32(r, c + 1)];
+        af[i][0] = x.x; af[i][1] = x.y; af[i][2] = x.z; af[i][3] = x.w;
+        af[i][4] = y.x; af[i][5] = y.y; af[i][6] = y.z; af[i][7] = y.w;
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        int r = wn * WN + j * 32 + lrow;
+        float4 x = *(const float4*)&Bs[cur][swz32(r, c)];
+        float4 y = *(const float4*)&Bs[cur][swz32(r, c + 1)];
+        bf[j][0] = x.x; bf[j][1] = x.y; bf[j][2] = x.z; bf[j][3] = x.w;
+        bf[j][4] = y.x; bf[j][5] = y.y; bf[j][6] = y.z; bf[j][7] = y.w;
+      }
+#pragma unroll
+      for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][t], bf[j][t], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int col = n0 + wn * WN + j * 32 + lrow;
+    if (col >= a.N) continue;
+    const float bias = a.bias ? load_f(a.bias, a.bias_dtype, col) : 0.f;
+    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + col) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        if (row < a.M) epilogue_one(a, bidx, row, col, acc[i][j][r], bias, gate);
+      }
+  }
+}
+
+// ---- GEMV ---------------------------------------------------------------------
+
+// M <= 4 rows: the rows go to LDS as fp32, each wave produces 4 output
+// features, lanes stride K in runs of 8 so every weight load is 16 bytes.
+template <int MR>
+__global__ __launch_bounds__(256) void gemv_kernel(GemmArgs a) {
+  extern __shared__ float xs[];  // [MR][K]
+  const int64_t bidx = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < MR * a.K; i += 256) {
+    int m = i / a.K, k = i % a.K;
+    xs[i] = m < a.M ? load_f(a.a, a.a_dtype, bidx * a.batch_a + int64_t(m) * a.lda + k) : 0.f;
+  }
+  __syncthreads();
+  const char* W = (const char*)a.w;
+  const int nbase = blockIdx.x * 16 + wave * 4;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int n = nbase + q;
+    if (n >= a.N) break;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = 0.f;
+    for (int k = lane * 8; k < a.K; k += 512) {
+      float w[8];
+      load_w8(a, W, n, k, w);
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[m] += xs[m * a.K + k + e] * w[e];
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float v = wave_sum(acc[m]);
+      if (lane == 0 && m < a.M) {
+        const float bias = a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f;
+        const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + n) : 0.f;
+        epilogue_one(a, bidx, m, n, v, bias, gate);
+      }
+    }
+  }
+}
+
+// ---- generic (DmlOps.Gemm, any layout) ----------------------------------------
+
+__global__ void gemm_generic_kernel(GemmGenericArgs g) {
+  const int64_t total = g.batch0 * g.batch1 * g.M * g.N;
+  for (int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; id < total;
+       id += int64_t(gridDim.x) * blockDim.x) {
+    int64_t n = id % g.N, r = id / g.N;
+    int64_t m = r % g.M;
+    r /= g.M;
+    int64_t b1 = r % g.batch1, b0 = r / g.batch1;
+    const int64_t ao = b0 * g.va.stride[0] + b1 * g.va.stride[1];
+    const int64_t bo = b0 * g.vb.stride[0] + b1 * g.vb.stride[1];
+    float acc = 0.f;
+    for (int64_t k = 0; k < g.K; k++) {
+      int64_t ai = g.trans_a ? k * g.va.stride[2] + m * g.va.stride[3] : m * g.va.stride[2] + k * g.va.stride[3];
+      int64_t bi = g.trans_b ? n * g.vb.stride[2] + k * g.vb.stride[3] : k * g.vb.stride[2] + n * g.vb.stride[3];
+      acc += load_f(g.a, g.a_dtype, ao + ai) * load_f(g.b, g.b_dtype, bo + bi);
+    }
+    float v = g.alpha * acc;
+    if (g.c) {
+      int64_t ci = b0 * g.vc.stride[0] + b1 * g.vc.stride[1] + m * g.vc.stride[2] + n * g.vc.stride[3];
+      v += g.beta * load_f(g.c, g.c_dtype, ci);
+    }
+    store_f(g.out, g.out_dtype, id, v);
+  }
+}
+
+void launch_gemm_generic(const GemmGenericArgs& g, hipStream_t s) {
+  int64_t total = g.batch0 * g.batch1 * g.M * g.N;
+  int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(gemm_generic_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, s, g);
+}
+
+// ---- dispatch -----------------------------------------------------------------
+
+enum GemmKind { K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_F32, K_GENERIC_LINEAR };
+
+// Whether every 16-byte (or 8-byte, int8 GEMV) vector load a kernel makes
+// of the weight / the activation rows is aligned.
+static bool w_aligned(const GemmArgs& a) {
+  const int es = a.w_dtype == NDX_I8 ? 1 : dtype_size(a.w_dtype);
+  const int need = a.w_dtype == NDX_I8 ? 8 : 16;
+  return (uintptr_t)a.w % need == 0 && (a.ldw * es) % need == 0;
+}
+static bool a_aligned(const GemmArgs& a) {
+  const int es = dtype_size(a.a_dtype);
+  return (uintptr_t)a.a % 16 == 0 && (a.lda * es) % 16 == 0 && (a.batch_a * es) % 16 == 0;
+}
+
+static GemmKind choose(const GemmArgs& a) {
+  const int MR = a.M;
+  if (!w_aligned(a)) return K_GENERIC_LINEAR;
+  if (MR <= 4 && int64_t(4) * a.K * 4 <= 65536 && a.K % 8 == 0) return K_GEMV;
+  if (!a_aligned(a)) return K_GENERIC_LINEAR;
+  if (a.w_dtype == NDX_I8 && (uintptr_t)a.w % 16) return K_GENERIC_LINEAR;
+  if ((a.a_dtype == NDX_BF16 || a.a_dtype == NDX_F16) && a.K % 16 == 0) {
+    int64_t t256 = int64_t((a.M + 255) / 256) * ((a.N + 255) / 256) * a.batch;
+    int64_t t128 = int64_t((a.M + 127) / 128) * ((a.N + 127) / 128) * a.batch;
+    if (t256 >= 192) return K_MFMA_256;
+    if (t128 >= 160 || a.M > 64) return K_MFMA_128;
+    return K_MFMA_64;
+  }
+  if (a.a_dtype == NDX_F32 && a.K % 8 == 0) return K_F32;
+  return K_GENERIC_LINEAR;
+}
+
+const char* gemm_family(const GemmArgs& a) {
+  const bool i8 = a.w_dtype == NDX_I8;
+  switch (choose(a)) {
+    case K_GEMV: return "gemv";
+    case K_MFMA_256: return i8 ? "gemm_w8_mfma_256x256" : "gemm_mfma_256x256";
+    case K_MFMA_128: return i8 ? "gemm_w8_mfma_128x128" : "gemm_mfma_128x128";
+    case K_MFMA_64: return i8 ? "gemm_w8_mfma_64x128" : "gemm_mfma_64x128";
+    case K_F32: return "gemm_f32_mfma_128x128";
+    default: return "gemm_linear_generic";
+  }
+}
+
+__global__ void linear_generic_kernel(GemmArgs a) {
+  const int64_t total = int64_t(a.batch) * a.M * a.N;
+  for (int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; id < total;
+       id += int64_t(gridDim.x) * blockDim.x) {
+    int n = (int)(id % a.N);
+    int64_t r = id / a.N;
+    int m = (int)(r % a.M);
+    int64_t b = r / a.M;
+    float acc = 0.f;
+    for (int k = 0; k < a.K; k++) {
+      float w = a.w_dtype == NDX_I8
+                    ? float(((const int8_t*)a.w)[int64_t(n) * a.ldw + k]) *
+                          scale_at(a.scales, a.s_dtype, int64_t(n) * a.lds + k / a.qblock)
+                    : load_f(a.w, a.w_dtype, int64_t(n) * a.ldw + k);
+      acc += load_f(a.a, a.a_dtype, b * a.batch_a + int64_t(m) * a.lda + k) * w;
+    }
+    const float bias = a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f;
+    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, b * a.batch_gate + n) : 0.f;
+    epilogue_one(a, b, m, n, acc, bias, gate);
+  }
+}
+
+template <int BM, int BN, int WM, int WN>
+static void launch_mfma(const GemmArgs& a, hipStream_t s) {
+  int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  int grid = (tiles + 7) / 8 * 8;
+  dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
+  const bool i8 = a.w_dtype == NDX_I8;
+  if (a.a_dtype == NDX_BF16) {
+    if (i8) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, __bf16, true>), g, b, 0, s, a, grid);
+    else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, __bf16, false>), g, b, 0, s, a, grid);
+  } else {
+    if (i8) hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, _Float16, true>), g, b, 0, s, a, grid);
+    else hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, _Float16, false>), g, b, 0, s, a, grid);
+  }
+}
+
+void launch_gemm(const GemmArgs& a, hipStream_t s) {
+  if (a.M == 0 || a.N == 0 || a.batch == 0) return;
+  switch (choose(a)) {
+    case K_GEMV: {
+      dim3 g((a.N + 15) / 16, a.batch);
+      size_t lds = size_t(4) * a.K * sizeof(float);
+      if (a.M == 1) hipLaunchKernelGGL(gemv_kernel<1>, g, dim3(256), lds / 4, s, a);
+      else if (a.M == 2) hipLaunchKernelGGL(gemv_kernel<2>, g, dim3(256), lds / 2, s, a);
+      else hipLaunchKernelGGL(gemv_kernel<4>, g, dim3(256), lds, s, a);
+      break;
+    }
+    case K_MFMA_256: launch_mfma<256, 256, 128, 128>(a, s); break;
+    case K_MFMA_128: launch_mfma<128, 128, 64, 64>(a, s); break;
+    case K_MFMA_64: launch_mfma<64, 128, 32, 64>(a, s); break;
+    case K_F32: {
+      int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+      int grid = (tiles + 7) / 8 * 8;
+      hipLaunchKernelGGL(gemm_f32_kernel, dim3(grid, a.batch), dim3(256), 0, s, a, grid);
+      break;
+    }
+    default: {
+      int64_t total = int64_t(a.batch) * a.M * a.N;
+      int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
+      hipLaunchKernelGGL(linear_generic_kernel, dim3(blocks), dim3(256), 0, s, a);
+    }
+  }
+}
+
+}  // namespace ndx

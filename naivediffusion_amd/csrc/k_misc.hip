@@ -1,0 +1,173 @@
+// Bandwidth-bound helpers: the strided elementwise kernel (casts, views made
+// packed, activations, scale/bias, binary arithmetic), nearest upsampling,
+// patchify, the synthetic normal fill and the device int8 quantiser.
+
+#include "k_common.h"
+
+namespace ndx {
+
+struct Idx4 {
+  int64_t size[4];
+};
+
+__device__ __forceinline__ int64_t offset_of(const View4& v, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+  return i0 * v.stride[0] + i1 * v.stride[1] + i2 * v.stride[2] + i3 * v.stride[3];
+}
+
+__device__ __forceinline__ float apply_elem(int op, float a, float b, float scale, float bias) {
+  switch (op) {
+    case ELEM_COPY: return a;
+    case ELEM_SIGMOID: return sigmoid_f(a);
+    case ELEM_SILU: return silu_f(a);
+    case ELEM_GELU: return gelu_f(a);
+    case ELEM_TANH: return tanhf(a);
+    case ELEM_GELU_TANH: return gelu_tanh_f(a);
+    case ELEM_SCALE_BIAS: return a * scale + bias;
+    case ELEM_ADD: return a + b;
+    case ELEM_SUB: return a - b;
+    case ELEM_MUL: return a * b;
+    case ELEM_DIV: return a / b;
+    default: return a;
+  }
+}
+
+// One thread per output element of a 4-D strided view; the innermost axis
+// is the fastest so packed tensors read and write coalesced.
+__global__ void elementwise_kernel(ElemArgs a, int64_t total) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t step = int64_t(gridDim.x) * blockDim.x;
+  const int64_t s3 = a.vo.size[3], s2 = a.vo.size[2], s1 = a.vo.size[1];
+  for (; i < total; i += step) {
+    int64_t r = i;
+    int64_t i3 = r % s3;
+    r /= s3;
+    int64_t i2 = r % s2;
+    r /= s2;
+    int64_t i1 = r % s1;
+    int64_t i0 = r / s1;
+    float x = load_f(a.in0, a.dt0, offset_of(a.v0, i0, i1, i2, i3));
+    float y = a.in1 ? load_f(a.in1, a.dt1, offset_of(a.v1, i0, i1, i2, i3)) : 0.f;
+    store_f(a.out, a.dto, offset_of(a.vo, i0, i1, i2, i3), apply_elem(a.op, x, y, a.scale, a.bias));
+  }
+}
+
+static int grid_for(int64_t total, int threads) {
+  int64_t blocks = (total + threads - 1) / threads;
+  if (blocks > 65536 * 8) blocks = 65536 * 8;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+void launch_elementwise(const ElemArgs& a, hipStream_t s) {
+  int64_t total = a.vo.size[0] * a.vo.size[1] * a.vo.size[2] * a.vo.size[3];
+  if (total == 0) return;
+  hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
+}
+
+__global__ void upsample_kernel(UpsampleArgs a, int64_t total) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t step = int64_t(gridDim.x) * blockDim.x;
+  const int64_t Wo = a.W * a.scale, Ho = a.H * a.scale;
+  for (; i < total; i += step) {
+    int64_t r = i;
+    int64_t x = r % Wo;
+    r /= Wo;
+    int64_t y = r % Ho;
+    r /= Ho;
+    int64_t c = r % a.C;
+    int64_t n = r / a.C;
+    float v = load_f(a.x, a.dtype, offset_of(a.vx, n, c, y / a.scale, x / a.scale));
+    store_f(a.y, a.dtype, i, v);
+  }
+}
+
+void launch_upsample(const UpsampleArgs& a, hipStream_t s) {
+  int64_t total = a.N * a.C * a.H * a.scale * a.W * a.scale;
+  hipLaunchKernelGGL(upsample_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
+}
+
+// [N, C, H, W] <-> [N, (H/p)(W/p), C p p] with feature order (c, dy, dx).
+__global__ void patch_kernel(PatchArgs a, int64_t total) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t step = int64_t(gridDim.x) * blockDim.x;
+  const int p = a.p, hp = a.H / p, wp = a.W / p;
+  const int64_t feat = int64_t(a.C) * p * p;
+  const int64_t per = int64_t(a.C) * a.H * a.W;
+  for (; i < total; i += step) {
+    // i indexes the token layout.
+    int64_t n = i / per, j = i % per;
+    int64_t token = j / feat, f = j % feat;
+    int64_t ty = token / wp, tx = token % wp;
+    int64_t c = f / (p * p), dy = (f / p) % p, dx = f % p;
+    int64_t img = n * per + (c * a.H + ty * p + dy) * a.W + tx * p + dx;
+    if (!a.inverse)
+      store_f(a.y, a.y_dtype, i, load_f(a.x, a.x_dtype, img));
+    else
+      store_f(a.y, a.y_dtype, img, load_f(a.x, a.x_dtype, i));
+  }
+  (void)hp;
+}
+
+void launch_patch(const PatchArgs& a, hipStream_t s) {
+  int64_t total = int64_t(a.N) * a.C * a.H * a.W;
+  hipLaunchKernelGGL(patch_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
+}
+
+__global__ void fill_normal_kernel(void* p, int dt, int64_t n, uint64_t seed, float mean, float sd) {
+  int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t step = int64_t(gridDim.x) * blockDim.x;
+  for (; i < n; i += step) {
+    uint64_t h1 = splitmix64(seed ^ splitmix64(2ull * uint64_t(i)));
+    uint64_t h2 = splitmix64(seed ^ splitmix64(2ull * uint64_t(i) + 1ull));
+    double u1 = (double((h1 >> 11) + 1ull)) * (1.0 / 9007199254740992.0);  // (0, 1]
+    double u2 = double(h2 >> 11) * (1.0 / 9007199254740992.0);            // [0, 1)
+    double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    float v = (float)(double(mean) + double(sd) * z);
+    store_f(p, dt, i, v);
+  }
+}
+
+void launch_fill_normal(void* ptr, int dtype, int64_t n, uint64_t seed, float mean, float std,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, ptr, dtype, n, seed, mean, std);
+}
+
+// One thread per (row, block): the rule of Tensors/BlockQuantizer.cs:55-72.
+__global__ void quantize_kernel(const void* w, int wdt, int64_t rows, int64_t cols, int block, int sdt,
+                                int8_t* q, void* scales) {
+  int64_t blocks = cols / block;
+  int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= rows * blocks) return;
+  int64_t r = id / blocks, b = id % blocks;
+  int64_t start = r * cols + b * block;
+  float peak = 0.f;
+  for (int i = 0; i < block; i++) peak = fmaxf(peak, fabsf(load_f(w, wdt, start + i)));
+  float stored;
+  if (sdt == NDX_F16) {
+    _Float16 h = (_Float16)(peak / 127.0f);
+    ((_Float16*)scales)[id] = h;
+    stored = (float)h;
+  } else {
+    stored = peak / 127.0f;
+    ((float*)scales)[id] = stored;
+  }
+  if (stored == 0.f) {
+    for (int i = 0; i < block; i++) q[start + i] = 0;
+    return;
+  }
+  float inverse = 1.0f / stored;
+  for (int i = 0; i < block; i++) {
+    float v = rintf(load_f(w, wdt, start + i) * inverse);
+    v = fminf(127.f, fmaxf(-127.f, v));
+    q[start + i] = (int8_t)(int)v;
+  }
+}
+
+void launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int block, int s_dtype, int8_t* q,
+                     void* scales, hipStream_t s) {
+  int64_t n = rows * (cols / block);
+  int blocks = (int)((n + 255) / 256);
+  hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, s, w, w_dtype, rows, cols, block, s_dtype, q, scales);
+}
+
+}  // namespace ndx

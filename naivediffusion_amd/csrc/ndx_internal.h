@@ -1,0 +1,197 @@
+// Internal declarations shared by the runtime (runtime.cpp, graph.cpp) and
+// the kernel files (k_*.hip). Nothing here crosses the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/ndx.h"
+
+namespace ndx {
+
+// ---- element types ---------------------------------------------------------
+
+__host__ __device__ inline int dtype_size(int dt) {
+  switch (dt) {
+    case NDX_F32: case NDX_U32: case NDX_I32: return 4;
+    case NDX_F16: case NDX_BF16: case NDX_U16: return 2;
+    case NDX_I64: return 8;
+    case NDX_I8: return 1;
+    default: return 0;
+  }
+}
+__host__ __device__ inline bool dtype_is_float(int dt) { return dt == NDX_F32 || dt == NDX_F16 || dt == NDX_BF16; }
+const char* dtype_name(int dt);
+
+// ---- errors ----------------------------------------------------------------
+
+// Thrown inside the library, turned into an ndx_status at the C boundary.
+struct Error {
+  ndx_status status;
+  std::string message;
+};
+[[noreturn]] void fail(ndx_status status, const std::string& message);
+void set_last_error(const std::string& message);
+// Checks a HIP call; out-of-memory becomes NDX_OOM, anything else DEVICE_LOST.
+void hip_check(hipError_t err, const char* what);
+
+// ---- strided 4-D views -----------------------------------------------------
+
+// Every tensor inside the library is a 4-D view: sizes outermost first,
+// strides in elements (0 repeats an axis), like DmlTensorDesc.
+struct View4 {
+  int64_t size[4];
+  int64_t stride[4];
+};
+
+// ---- kernel launch arguments ------------------------------------------------
+
+enum Epilogue {
+  EPI_NONE = NDX_EPI_NONE,
+  EPI_GELU_TANH = NDX_EPI_GELU_TANH,
+  EPI_GELU = NDX_EPI_GELU,
+  EPI_SILU = NDX_EPI_SILU,
+  EPI_GATED_RESIDUAL = NDX_EPI_GATED_RESIDUAL,
+  EPI_RESIDUAL = NDX_EPI_RESIDUAL,
+};
+
+// One linear layer's product: C[b] = epi(A[b] (M x K, rows lda apart) *
+// W^T (W is N x K, rows ldw apart) + bias). W may be int8 with per-(row,
+// block) scales. gate is a per-batch [N] row; resid is [b][M][N] (ldr).
+struct GemmArgs {
+  const void* a; int64_t lda; int64_t batch_a; int a_dtype;
+  const void* w; int64_t ldw; int64_t batch_w; int w_dtype;
+  const void* scales; int64_t lds; int qblock; int s_dtype;  // int8 weights only
+  void* c; int64_t ldc; int64_t batch_c; int c_dtype;
+  const void* bias; int bias_dtype;
+  const void* gate; int64_t batch_gate; int gate_dtype;
+  const void* resid; int64_t ldr; int64_t batch_r; int r_dtype;
+  int M, N, K, batch;
+  int epilogue;
+};
+
+// DmlOps.Gemm in full generality (any strides, transposes, alpha, beta): a
+// plain fp32-accumulating kernel for the small cases the builder emits.
+struct GemmGenericArgs {
+  const void* a; View4 va; int a_dtype;
+  const void* b; View4 vb; int b_dtype;
+  const void* c; View4 vc; int c_dtype;  // may be null
+  void* out; int out_dtype;
+  int64_t M, N, K;  // per (d0, d1) batch
+  int64_t batch0, batch1;
+  int trans_a, trans_b;
+  float alpha, beta;
+};
+
+// Attention over packed [B, T, H*d] rows: each of q, k, v, out may come in two
+// row segments (the image and the text stream of a joint sequence) so that a
+// join feeding the attention costs no copy.
+struct AttnSeg {
+  const void* ptr[2];
+  int64_t rows0;       // rows in the first segment; the rest in the second
+  int64_t ld[2];       // row stride (elements) of each segment
+  int64_t batch[2];    // batch stride (elements) of each segment
+};
+struct AttnArgs {
+  AttnSeg q, k, v;
+  void* out[2]; int64_t out_rows0; int64_t out_ld[2]; int64_t out_batch[2];
+  int B, T, S, H, d, dv;
+  float scale;
+  int dtype;            // F32, BF16 or F16 for q/k/v/out
+  int mask_kind;
+  const int32_t* mask;  // key length (1 value) or boolean table
+  int64_t mask_stride[4];  // [b, h, t, s] element strides of the boolean table
+};
+
+struct HeadNormRotateArgs {
+  const void* x; int64_t ldx; int64_t batch_x; int x_dtype;
+  void* y; int64_t ldy; int64_t batch_y; int y_dtype;
+  const void* weight; int w_dtype;      // [d] or null
+  const float* cos; const float* sin;   // [T, d/2] or null
+  int B, T, H, d;
+  float eps;
+};
+
+struct RowNormArgs {
+  // LayerNorm / Modulate / RmsNorm over the last axis of [rows, D].
+  const void* x; int64_t ldx; int64_t batch_x; int x_dtype;
+  void* y; int64_t ldy; int y_dtype;
+  int64_t rows; int D;
+  int64_t rows_per_batch;            // batch index = row / rows_per_batch
+  const void* weight; int64_t batch_w; int w_dtype;   // LN weight / (1+scale) / RMS weight
+  const void* bias; int64_t batch_b; int b_dtype;     // LN bias / shift
+  float eps;
+  int mode;   // 0 layernorm(+affine), 1 modulate, 2 rmsnorm
+};
+
+struct GroupNormArgs {
+  const void* x; void* y; int dtype; int y_dtype;
+  int N, C, HW, groups;
+  const void* weight; const void* bias; int w_dtype;
+  float eps;
+  int silu;
+};
+
+struct ConvArgs {
+  const void* x; int x_dtype;  // [N, Cin, H, W] packed
+  const void* w; int w_dtype;  // [Cout, Cin, kh, kw] packed (or int8 + scales)
+  const void* scales; int qblock; int s_dtype;
+  const void* bias; int bias_dtype;
+  const void* resid;           // [N, Cout, Ho, Wo] packed, same dtype as y
+  void* y; int y_dtype;
+  int N, Cin, H, W, Cout, kh, kw, stride, pad, Ho, Wo;
+};
+
+// Generic strided elementwise: out = f(in0, in1) over a 4-D shape.
+enum ElemOp {
+  ELEM_COPY = 0,       // cast/identity/pack
+  ELEM_SIGMOID, ELEM_SILU, ELEM_GELU, ELEM_TANH, ELEM_GELU_TANH,
+  ELEM_SCALE_BIAS,
+  ELEM_ADD, ELEM_SUB, ELEM_MUL, ELEM_DIV,
+};
+struct ElemArgs {
+  const void* in0; View4 v0; int dt0;
+  const void* in1; View4 v1; int dt1;
+  void* out; View4 vo; int dto;
+  int op;
+  float scale, bias;
+};
+
+struct UpsampleArgs {
+  const void* x; View4 vx; void* y; int dtype; int scale;
+  int64_t N, C, H, W;
+};
+struct PatchArgs {
+  const void* x; void* y; int x_dtype; int y_dtype;
+  int N, C, H, W, p;
+  int inverse;
+};
+
+// ---- launchers (defined in the k_*.hip files) ---------------------------------
+
+void launch_gemm(const GemmArgs& a, hipStream_t s);
+void launch_gemm_generic(const GemmGenericArgs& a, hipStream_t s);
+void launch_attention(const AttnArgs& a, hipStream_t s);
+void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s);
+void launch_row_norm(const RowNormArgs& a, hipStream_t s);
+void launch_group_norm(const GroupNormArgs& a, hipStream_t s);
+void launch_conv2d(const ConvArgs& a, hipStream_t s);
+void launch_elementwise(const ElemArgs& a, hipStream_t s);
+void launch_upsample(const UpsampleArgs& a, hipStream_t s);
+void launch_patch(const PatchArgs& a, hipStream_t s);
+void launch_fill_normal(void* ptr, int dtype, int64_t n, uint64_t seed, float mean, float std,
+                        hipStream_t s);
+void launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int block,
+                     int s_dtype, int8_t* q, void* scales, hipStream_t s);
+
+// Host quantiser (runtime.cpp), shared by ndx_quantize_block_int8 and the
+// graph's ModelBuilder.Weight path.
+void quantize_host(const void* w, int dtype, int64_t rows, int64_t cols, int block, int s_dtype,
+                   int8_t* q, void* scales);
+
+// Which GEMM kernel a shape goes to, and the algorithmic work, for profiling.
+const char* gemm_family(const GemmArgs& a);
+
+}  // namespace ndx

@@ -1,0 +1,409 @@
+"""GPU parity of each kernel family against the oracle, through the C ABI
+(ModelBuilder -> ndx_graph_* -> libndx.so): the linear layer's GEMMs at the
+MMDiT block's shapes and at ragged ones, int8 weights, attention with its
+masks and segmented (joined) operands, the norm kernels, and the smoke
+cases of the reference (Cli/SmokeTest.cs). Tolerances: max|gpu - oracle| /
+max|oracle| <= 2e-2 at bf16/f16 compute and 1e-3 at fp32 (the measure of
+QuantProbe.cs:50-57); integer work bit-exact."""
+
+import math
+
+import numpy as np
+import pytest
+
+import naivediffusion_amd as nd
+import oracle
+from naivediffusion_amd import rng
+from naivediffusion_amd.graph import Ops
+from naivediffusion_amd.layers import Layers, Transformer
+from naivediffusion_amd.tensors import HostDataType as DT, HostTensor, bf16_to_f32, f32_to_bf16
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL, F32_TOL = 2e-2, 1e-3
+
+
+def bf(x):
+    """x rounded to bf16, as fp32 values."""
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
+
+
+def normal(name, shape, std=1.0):
+    return rng.normal(rng.tensor_seed(7, name), shape, 0.0, std)
+
+
+def run(model, *inputs):
+    return [t.ToFloats() for t in model.Run(*inputs)]
+
+
+# ---- linear ------------------------------------------------------------------------
+
+LINEAR_CASES = [
+    # (M, K, N, batch): the MMDiT block at 1024 + 128 tokens, the text stream,
+    # the adaLN GEMV, and ragged shapes that leave partial tiles everywhere.
+    (1024, 3072, 3072, 1),
+    (1024, 3072, 12288, 1),
+    (1024, 12288, 3072, 1),
+    (128, 3072, 9216, 1),
+    (1, 3072, 18432, 1),
+    (2, 256, 3072, 1),
+    (1000, 320, 257, 1),
+    (77, 64, 96, 2),
+    (5376 // 8, 64, 3072, 1),
+]
+
+
+@pytest.mark.parametrize("M,K,N,B", LINEAR_CASES)
+@pytest.mark.parametrize("compute", [DT.BFloat16, DT.Float32])
+def test_linear_against_oracle(device, M, K, N, B, compute):
+    print(f"[gpu] linear M={M} K={K} N={N} B={B} {compute.name}", flush=True)
+    x = bf(normal("x", (B, 1, M, K)))
+    w = bf(normal("w", (N, K), 0.02))
+    b = bf(normal("b", (N,), 0.02))
+    model = nd.ModelBuilder(device, compute)
+    xin = model.Placeholder([B, 1, M, K], compute)
+    y = Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b))
+    model.Compile([y])
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(compute))[0]
+    ref = oracle.linear(x, w, b)
+    assert out.shape == ref.shape
+    err = rel_err(out, ref)
+    print(f"[gpu]   rel err {err:.2e}", flush=True)
+    assert err <= (BF16_TOL if compute == DT.BFloat16 else F32_TOL)
+
+
+@pytest.mark.parametrize("epi", ["gelu_tanh", "gelu", "silu", "gated", "residual"])
+def test_linear_epilogues(device, epi):
+    M, K, N = 300, 512, 384
+    x = bf(normal("ex", (1, 1, M, K)))
+    w = bf(normal("ew", (N, K), 0.05))
+    b = bf(normal("eb", (N,), 0.05))
+    res = normal("er", (1, 1, M, N))
+    gate = normal("eg", (1, 1, 1, N))
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    xin = model.Placeholder([1, 1, M, K])
+    rin = model.Placeholder([1, 1, M, N], DT.Float32)
+    gin = model.Placeholder([1, 1, 1, N], DT.Float32)
+    kw = {}
+    if epi in ("gelu_tanh", "gelu", "silu"):
+        kw["activation"] = epi
+    elif epi == "gated":
+        kw.update(gate=gin, residual=rin)
+    else:
+        kw.update(residual=rin)
+    y = Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b), **kw)
+    model.Compile([y])
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16), HostTensor.FromFloats(res),
+              HostTensor.FromFloats(gate))[0]
+    p = oracle.linear(x, w, b)
+    ref = {"gelu_tanh": lambda: oracle.gelu_tanh(p), "gelu": lambda: oracle.gelu(p), "silu": lambda: oracle.silu(p),
+           "gated": lambda: res + gate * p, "residual": lambda: res + p}[epi]()
+    assert rel_err(out, ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("compute", [DT.BFloat16, DT.Float32])
+@pytest.mark.parametrize("M", [1, 256, 1024])
+def test_int8_linear_against_oracle(device, compute, M):
+    """ModelBuilder.Weight under int8 (Graph/ModelBuilder.cs:65-88): the GEMM
+    matches the oracle's product with the dequantised weights, and stays
+    within the bf16 bound of the unquantised product."""
+    print(f"[gpu] int8 linear M={M} {compute.name}", flush=True)
+    K, N = 3072, 3072
+    x = bf(normal("qx", (1, 1, M, K)))
+    w = bf(normal("qw", (N, K), 0.02))
+    model = nd.ModelBuilder(device, compute, int8Weights=True)
+    xin = model.Placeholder([1, 1, M, K], compute)
+    model.Compile([Layers.Linear(model, xin, HostTensor.FromFloats(w))])
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(compute))[0]
+    q, s = oracle.quantize(w, N)
+    deq = (q.astype(np.float32).reshape(N, K // 32, 32) *
+           oracle.f16_bits_to_f32(s)[:, :, None]).reshape(N, K)
+    assert rel_err(out, oracle.linear(x, deq)) <= (BF16_TOL if compute == DT.BFloat16 else F32_TOL)
+    assert rel_err(out, oracle.linear(x, w)) <= BF16_TOL
+
+
+def test_device_quantizer_is_bit_exact_with_the_oracle(device):
+    w = bf(normal("dq", (640, 3072), 0.02))
+    wt = device.Upload(HostTensor.FromFloats(w).ConvertTo(DT.BFloat16))
+    q = device.Empty(DT.Int8, [640, 3072])
+    s = device.Empty(DT.Float16, [640, 96])
+    nd._lib.call("ndx_quantize_block_int8_device", wt.handle, 32, int(DT.Float16), q.handle, s.handle)
+    oq, os_ = oracle.quantize(w, 640)
+    assert np.array_equal(q.Download().Data, oq)
+    assert np.array_equal(s.Download().Data.view(np.uint16), os_)
+
+
+# ---- attention -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,S,H,d,dtype", [
+    (1152, 1152, 24, 128, DT.BFloat16),
+    (300, 77, 10, 64, DT.Float16),
+    (130, 517, 4, 128, DT.BFloat16),
+    (257, 257, 2, 128, DT.Float32),
+    (64, 100, 3, 64, DT.Float32),
+])
+def test_attention_against_oracle(device, T, S, H, d, dtype):
+    print(f"[gpu] attention T={T} S={S} H={H} d={d} {dtype.name}", flush=True)
+    q = bf(normal("aq", (1, T, H * d)))
+    k = bf(normal("ak", (1, S, H * d)))
+    v = bf(normal("av", (1, S, H * d)))
+    model = nd.ModelBuilder(device, dtype)
+    ins = [model.Placeholder([1, 1, n, H * d]) for n in (T, S, S)]
+    model.Compile([Layers.Attend(*ins, H)])
+    out = run(model, *[HostTensor.FromFloats(a.reshape(1, 1, -1, H * d)).ConvertTo(dtype) for a in (q, k, v)])[0]
+    ref = oracle.mha(q, k, v, H)
+    err = rel_err(out.reshape(ref.shape), ref)
+    print(f"[gpu]   rel err {err:.2e}", flush=True)
+    assert err <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
+
+
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float32])
+def test_attention_masks(device, dtype):
+    """Key-length and boolean masks with DirectML's -10000 (DmlOps.cs:483);
+    the causal table of QwenImageConditioner.cs:69-80 broadcast over heads."""
+    T, H, d = 200, 2, 128
+    q, k, v = (bf(normal(n, (1, T, H * d))) for n in ("mq", "mk", "mv"))
+    table = oracle.causal_table(150, T).reshape(1, 1, T, T)
+    model = nd.ModelBuilder(device, dtype)
+    ins = [model.Placeholder([1, 1, T, H * d]) for _ in range(3)]
+    kl = model.Placeholder([1, 1, 1, 1], DT.Int32)
+    tb = model.Placeholder([1, 1, T, T], DT.Int32)
+    a1 = Layers.Attend(*ins, H, kl, nd.MaskType.KeySequenceLength)
+    a2 = Layers.Attend(*ins, H, Layers.Broadcast(tb, [1, H, T, T]), nd.MaskType.Boolean)
+    model.Compile([a1, a2])
+    host = [HostTensor.FromFloats(a.reshape(1, 1, T, H * d)).ConvertTo(dtype) for a in (q, k, v)]
+    o1, o2 = run(model, *host, HostTensor.FromInt32(np.array([137]), 1, 1, 1, 1), HostTensor.FromInt32(table))
+    tol = F32_TOL if dtype == DT.Float32 else BF16_TOL
+    assert rel_err(o1.reshape(1, T, -1), oracle.mha(q, k, v, H, mask_kind=1, key_len=137)) <= tol
+    assert rel_err(o2.reshape(1, T, -1), oracle.mha(q, k, v, H, mask_kind=2, mask=table)) <= tol
+
+
+def test_attention_reads_joined_streams_in_place(device):
+    """A join of the image and text rows feeding the attention is read as
+    two row segments; the result equals attention over the packed join."""
+    ni, nt, H, d = 300, 45, 4, 128
+    parts = {n: bf(normal(n, (1, 1, r, H * d))) for n, r in
+             (("qi", ni), ("qt", nt), ("ki", ni), ("kt", nt), ("vi", ni), ("vt", nt))}
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    ph = {n: model.Placeholder(list(a.shape)) for n, a in parts.items()}
+    j = [Ops.Join([ph[a], ph[b]], 2) for a, b in (("qi", "qt"), ("ki", "kt"), ("vi", "vt"))]
+    model.Compile([Layers.Attend(*j, H)])
+    out = run(model, *[HostTensor.FromFloats(a).ConvertTo(DT.BFloat16) for a in parts.values()])[0]
+    cat = [np.concatenate([parts[a], parts[b]], 2).reshape(1, ni + nt, H * d)
+           for a, b in (("qi", "qt"), ("ki", "kt"), ("vi", "vt"))]
+    assert rel_err(out.reshape(1, ni + nt, -1), oracle.mha(*cat, H)) <= BF16_TOL
+
+
+# ---- norms ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("out_dtype", [DT.BFloat16, DT.Float32])
+def test_modulate_against_oracle(device, out_dtype):
+    rows, D = 1000, 3072
+    x = normal("mx", (1, 1, rows, D)) * 3 + 1
+    shift, scale = normal("ms", (1, 1, 1, D), 0.5), normal("mc", (1, 1, 1, D), 0.5)
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    xi = model.Placeholder([1, 1, rows, D], DT.Float32)
+    si = model.Placeholder([1, 1, 1, D], DT.Float32)
+    ci = model.Placeholder([1, 1, 1, D], DT.Float32)
+    model.Compile([Transformer.Modulate(xi, si, ci, 1e-6, out_dtype)])
+    out = run(model, *map(HostTensor.FromFloats, (x, shift, scale)))[0]
+    ref = oracle.modulate(x.reshape(rows, D), shift.ravel(), scale.ravel(), 1e-6)
+    assert rel_err(out.reshape(rows, D), ref) <= (BF16_TOL / 4 if out_dtype == DT.BFloat16 else 1e-5)
+
+
+@pytest.mark.parametrize("D", [64, 640, 3072, 4096, 10240])
+def test_layer_and_rms_norm(device, D):
+    rows = 37
+    x = normal("nx", (1, 1, rows, D)) * 2 + 0.5
+    w, b = normal("nw", (D,), 0.3) + 1, normal("nb", (D,), 0.3)
+    model = nd.ModelBuilder(device, DT.Float32)
+    xi = model.Placeholder([1, 1, rows, D])
+    ln = Layers.LayerNorm(model, xi, HostTensor.FromFloats(w), HostTensor.FromFloats(b), 1e-5)
+    rms = Layers.RmsNorm(model, xi, HostTensor.FromFloats(w), 1e-6)
+    model.Compile([ln, rms])
+    o1, o2 = run(model, HostTensor.FromFloats(x))
+    assert rel_err(o1.reshape(rows, D), oracle.layer_norm(x.reshape(rows, D), w, b, 1e-5)) <= 1e-5
+    assert rel_err(o2.reshape(rows, D), oracle.rms_norm(x.reshape(rows, D), w, 1e-6)) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float32])
+def test_head_norm_rotate_against_oracle(device, dtype):
+    T, H, d = 333, 24, 128
+    x = bf(normal("hx", (1, 1, T, H * d)) * 2)
+    w = bf(normal("hw", (d,), 0.2) + 1)
+    cos, sin = oracle.mmdit_rope_tables(9, 37, 0)
+    model = nd.ModelBuilder(device, dtype)
+    xi = model.Placeholder([1, 1, T, H * d])
+    ci = model.Placeholder([1, T, 1, 64], DT.Float32)
+    si = model.Placeholder([1, T, 1, 64], DT.Float32)
+    y = Transformer.HeadNormRotate(model, xi, HostTensor.FromFloats(w), H, 1e-6, ci, si, dtype)
+    # the reference's unfused composition of the same two steps
+    z = Transformer.Flat(Transformer.Rotate(Transformer.HeadNorm(model, xi, HostTensor.FromFloats(w), H, d, 1e-6),
+                                            ci, si, H, d, dtype), H * d)
+    model.Compile([y, z])
+    o1, o2 = run(model, HostTensor.FromFloats(x).ConvertTo(dtype), HostTensor.FromFloats(cos.reshape(1, T, 1, 64)),
+                 HostTensor.FromFloats(sin.reshape(1, T, 1, 64)))
+    ref = oracle.rope(oracle.rms_norm(x.reshape(T * H, d), w, 1e-6).reshape(T, H * d), H, cos, sin)
+    tol = BF16_TOL if dtype == DT.BFloat16 else F32_TOL
+    assert rel_err(o1.reshape(T, -1), ref) <= tol
+    assert rel_err(o2.reshape(T, -1), ref) <= tol
+
+
+# ---- the reference's smoke cases (Cli/SmokeTest.cs) ---------------------------------------
+
+def test_smoke_gemm_and_broadcast_weight(device):
+    # SmokeTest.Gemm (:66-91) and GemmBroadcastWeight (:93-119)
+    g = nd.Graph(device)
+    a = g.Input(DT.Float32, [1, 1, 2, 3])
+    b = g.Input(DT.Float32, [1, 1, 3, 4])
+    m = nd.CompiledModel(g, [Ops.Gemm(a, b)], device)
+    ad = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    bd = np.arange(12, dtype=np.float32).reshape(3, 4)
+    out = m.Dispatch([HostTensor.FromFloats(ad, 1, 1, 2, 3), HostTensor.FromFloats(bd, 1, 1, 3, 4)])[0]
+    assert np.max(np.abs(out.ToFloats().reshape(2, 4) - ad @ bd)) <= 1e-4
+
+    g = nd.Graph(device)
+    x = g.Input(DT.Float32, [2, 1, 2, 3])
+    w = g.Input(DT.Float32, [1, 1, 4, 3])
+    bw = Ops.Reinterpret(w, [2, 1, 4, 3], [0, 12, 3, 1])
+    m = nd.CompiledModel(g, [Ops.Gemm(x, bw, transB=True)], device)
+    xd = np.arange(12, dtype=np.float32).reshape(2, 2, 3)
+    wd = (np.arange(12) % 5 - 2).astype(np.float32).reshape(4, 3)
+    out = m.Dispatch([HostTensor.FromFloats(xd, 2, 1, 2, 3), HostTensor.FromFloats(wd, 1, 1, 4, 3)])[0]
+    assert np.max(np.abs(out.ToFloats().reshape(2, 2, 4) - xd @ wd.T)) <= 1e-4
+
+
+def test_smoke_arithmetic_broadcast_transpose(device):
+    # SmokeTest.ScaleBiasAndArithmetic / BroadcastAdd / TransposeView (:121-190)
+    g = nd.Graph(device)
+    x = g.Input(DT.Float32, [1, 1, 1, 4])
+    y = 2.0 * x + 1.0
+    z = (x * y - x) / y
+    m = nd.CompiledModel(g, [z], device)
+    d = np.array([1, 2, 3, 4], np.float32)
+    out = m.Dispatch([HostTensor.FromFloats(d, 1, 1, 1, 4)])[0].ToFloats().ravel()
+    yy = 2 * d + 1
+    assert np.max(np.abs(out - (d * yy - d) / yy)) <= 1e-4
+
+    g = nd.Graph(device)
+    a = g.Input(DT.Float32, [1, 1, 3, 4])
+    row = g.Input(DT.Float32, [1, 1, 1, 4])
+    img = g.Input(DT.Float32, [1, 4, 2, 3])
+    m = nd.CompiledModel(g, [a + Layers.Broadcast(row, [1, 1, 3, 4]), Layers.ToTokens(img) * 1.0], device)
+    ad, rd = np.arange(12, dtype=np.float32), np.array([10, 20, 30, 40], np.float32)
+    imd = np.arange(24, dtype=np.float32)
+    o1, o2 = m.Dispatch([HostTensor.FromFloats(ad, 1, 1, 3, 4), HostTensor.FromFloats(rd, 1, 1, 1, 4),
+                         HostTensor.FromFloats(imd, 1, 4, 2, 3)])
+    assert np.array_equal(o1.ToFloats().reshape(3, 4), ad.reshape(3, 4) + rd)
+    assert np.array_equal(o2.ToFloats().reshape(6, 4), imd.reshape(4, 6).T)
+
+
+def test_smoke_group_norm_conv_join_upsample(device):
+    # SmokeTest.GroupNormalization (:208-239), Convolution (:241-281),
+    # JoinSliceUpsample (:308-335)
+    g = nd.Graph(device)
+    x = g.Input(DT.Float32, [1, 4, 1, 3])
+    grouped = Ops.Reinterpret(x, [1, 2, 2, 3])
+    gn = Ops.Reinterpret(Ops.MeanVarianceNormalization(grouped, [2, 3], 1e-5), [1, 4, 1, 3])
+    m = nd.CompiledModel(g, [gn], device)
+    data = np.array([1, 2, 3, 4, 5, 6, 0, 0, 0, 1, 1, 4], np.float32)
+    out = m.Dispatch([HostTensor.FromFloats(data, 1, 4, 1, 3)])[0].ToFloats().ravel()
+    assert np.max(np.abs(out - oracle.group_norm(data.reshape(1, 4, 1, 3), 2, eps=1e-5).ravel())) <= 1e-4
+
+    g = nd.Graph(device)
+    xi = g.Input(DT.Float32, [1, 1, 3, 3])
+    fi = g.Input(DT.Float32, [2, 1, 3, 3])
+    bi = g.Input(DT.Float32, [1, 2, 1, 1])
+    m = nd.CompiledModel(g, [Ops.Convolution(xi, fi, bi, [1, 1], [1, 1], [1, 1])], device)
+    f = np.zeros((2, 1, 3, 3), np.float32)
+    f[0, 0, 1, 1] = 1
+    f[1] = 1
+    xd = np.arange(9, dtype=np.float32).reshape(1, 1, 3, 3)
+    bias = np.array([0.5, -1], np.float32)
+    out = m.Dispatch([HostTensor.FromFloats(xd), HostTensor.FromFloats(f), HostTensor.FromFloats(bias, 1, 2, 1, 1)])
+    assert np.max(np.abs(out[0].ToFloats() - oracle.conv2d(xd, f, bias))) <= 1e-4
+
+    g = nd.Graph(device)
+    a = g.Input(DT.Float32, [1, 1, 2, 2])
+    b = g.Input(DT.Float32, [1, 1, 2, 2])
+    up = Ops.Upsample2D(Ops.Join([a, b], 1), 2, 2)
+    cropped = Ops.Slice(up, [0, 0, 0, 0], [1, 2, 3, 3], [1, 1, 1, 1])
+    m = nd.CompiledModel(g, [cropped], device)
+    ad, bd = np.array([1, 2, 3, 4], np.float32), np.array([5, 6, 7, 8], np.float32)
+    out = m.Dispatch([HostTensor.FromFloats(ad, 1, 1, 2, 2), HostTensor.FromFloats(bd, 1, 1, 2, 2)])[0]
+    exp = oracle.upsample_nearest(np.concatenate([ad, bd]).reshape(1, 2, 2, 2))[:, :, :3, :3]
+    assert np.array_equal(out.ToFloats(), exp)
+
+
+def test_smoke_owned_weights_cast_tanh(device):
+    # SmokeTest.OwnedWeights (:487-512), CastBothWays (:574-595), tanh (:498)
+    model = nd.ModelBuilder(device)
+    x = model.Placeholder([1, 1, 2, 2])
+    w = model.Constant(HostTensor.FromFloats(np.array([1, 0, 0, 2], np.float32), 1, 1, 2, 2))
+    model.Compile([Ops.Gemm(x, w)])
+    for rnd in range(2):
+        xd = np.array([1 + rnd, 2, 3, 4], np.float32)
+        out = model.Run(HostTensor.FromFloats(xd, 1, 1, 2, 2))[0].ToFloats().ravel()
+        assert np.array_equal(out, [xd[0], 2 * xd[1], xd[2], 2 * xd[3]])
+    g = nd.Graph(device)
+    x = g.Input(DT.Float32, [1, 1, 2, 4])
+    half = Ops.Cast(x, DT.Float16)
+    m = nd.CompiledModel(g, [half, Ops.Cast(half * 2.0, DT.Float32), Ops.ActivationTanh(x)], device)
+    data = ((np.random.default_rng(4).random(8) - 0.5) * 4).astype(np.float32)
+    o1, o2, o3 = m.Dispatch([HostTensor.FromFloats(data, 1, 1, 2, 4)])
+    rounded = data.astype(np.float16).astype(np.float32)
+    assert np.array_equal(o1.ToFloats().ravel(), rounded)
+    assert np.array_equal(o2.ToFloats().ravel(), (rounded * 2).astype(np.float16).astype(np.float32))
+    assert np.max(np.abs(o3.ToFloats().ravel() - np.tanh(data))) <= 1e-4
+
+
+def test_smoke_mixed_precision_block(device):
+    # SmokeTest.MixedPrecisionBlock (:778-813), at bf16 with tolerance 2e-2
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    x = model.Placeholder([1, 1, 3, 4], DT.Float32)
+    shift = model.Placeholder([1, 1, 1, 4], DT.Float32)
+    weight = ((np.random.default_rng(8).random(16) - 0.5)).astype(np.float32)
+    normed = Layers.Cast(Layers.LayerNorm(x, 1e-6) * 1.5 + Layers.Broadcast(shift, x.Shape), DT.BFloat16)
+    projected = Layers.Linear(model, normed, HostTensor.FromFloats(weight, 4, 4))
+    model.Compile([x + Layers.Cast(projected, DT.Float32) * 0.5])
+    data = ((np.random.default_rng(9).random(12) - 0.5) * 4).astype(np.float32)
+    sd = ((np.random.default_rng(10).random(4) - 0.5)).astype(np.float32)
+    out = model.Run(HostTensor.FromFloats(data, 1, 1, 3, 4), HostTensor.FromFloats(sd, 1, 1, 1, 4))[0].ToFloats()
+    n = oracle.modulate(data.reshape(3, 4), sd, np.full(4, 0.5, np.float32), 1e-6)
+    exp = data.reshape(3, 4) + oracle.linear(n, weight.reshape(4, 4)) * 0.5
+    assert np.max(np.abs(out.reshape(3, 4) - exp)) <= 2e-2
+
+
+def test_repeat_dispatch_is_bitwise_identical(device):
+    # SmokeTest.RmsNormHalfRepeats (:625-645): the first dispatch of a
+    # process must equal the second to the bit.
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    x = model.Placeholder([1, 256, 16, 128])
+    w = HostTensor.FromFloats(normal("rw", (128,), 0.4))
+    model.Compile([Layers.Cast(Layers.RmsNorm(model, x, w, 1e-6), DT.Float32),
+                   Layers.Attend(*[Ops.Reinterpret(x, [1, 1, 256, 2048])] * 3, 16)])
+    inp = HostTensor.FromFloats(normal("rx", (1, 256, 16, 128), 3)).ConvertTo(DT.BFloat16)
+    first = [t.Data.copy() for t in model.Run(inp)]
+    second = [t.Data.copy() for t in model.Run(inp)]
+    for a, b in zip(first, second):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def test_errors_leave_the_device_usable(device):
+    """OutOfVideoMemoryException leaves the device usable
+    (Dml/DmlDevice.cs:918-937): forced from the host, no GPU fault."""
+    device.SetFaultInjection(1)
+    with pytest.raises(nd.OutOfVideoMemoryError):
+        device.Empty(DT.Float32, [1024])
+    t = device.Upload(HostTensor.FromFloats(np.arange(4, dtype=np.float32)))
+    assert np.array_equal(t.Download().ToFloats(), np.arange(4, dtype=np.float32))
+    model = nd.ModelBuilder(device)
+    x = model.Placeholder([1, 1, 2, 2])
+    with pytest.raises(nd.InvalidOperationError, match="Compile"):
+        model.Run(HostTensor.FromFloats(np.zeros(4, np.float32), 1, 1, 2, 2))
+    model.Compile([x * 2.0])
+    with pytest.raises(nd.ArgumentError, match="expected 1 inputs"):
+        model.Run()
+    with pytest.raises(nd.ArgumentError):
+        model.Compiled.DispatchOnDevice([device.Upload(HostTensor.FromFloats(np.zeros(3, np.float32)))])
