@@ -64,8 +64,8 @@ __device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
+template <typename T, int D, int MASK>
+__global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, int grid) {
   typedef typename AMfma<T>::V V;
   constexpr int BQ = 128, BKEY = 64;
   constexpr int KCH = D / 8;                      // 16-byte chunks per key row
@@ -80,40 +80,35 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
   if (!attn_tile(blockIdx.x, grid, (a.T + BQ - 1) / BQ, a.H, a.B, qb, head, b)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 31, lh = lane >> 5;
-  const int q0 = qb * BQ + wave * 32;
-  const int qi = q0 + lq;
+  const int qi = qb * BQ + wave * 32 + lq;
   const int64_t col0 = int64_t(head) * D;
 
   // Q^T fragments, resident for the whole key loop.
   V qf[D / 16];
   {
-    const T* qrow = qi < a.T ? seg_row<T>(a.q, b, qi) + col0 : nullptr;
+    const T* qrow = seg_row<T>(a.q, b, min(qi, a.T - 1)) + col0;
 #pragma unroll
-    for (int s = 0; s < D / 16; s++) {
-      if (qrow)
-        qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
-      else
-        for (int e = 0; e < 8; e++) qf[s][e] = (T)0.f;
-    }
+    for (int s = 0; s < D / 16; s++) qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
   }
 
   uint4 rk[K_PER];
   uint4 rv[4];
-  const int vtask = tid;
-  const int vkg = vtask / (D / 8), vdc = vtask % (D / 8);
+  const int vkg = tid / (D / 8), vdc = tid % (D / 8);
   auto load_kv = [&](int kb) {
     const int key0 = kb * BKEY;
 #pragma unroll
     for (int i = 0; i < K_PER; i++) {
-      int id = tid + i * 256;
-      int key = id / KCH, c = id % KCH;
-      int gk = key0 + key;
-      rk[i] = gk < a.S ? *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8) : make_uint4(0, 0, 0, 0);
+      const int id = tid + i * 256;
+      const int key = id / KCH, c = id % KCH;
+      const int gk = min(key0 + key, a.S - 1);  // tail keys are masked below
+      rk[i] = *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8);
     }
-    if (vtask < V_TASKS) {
+    if (tid < V_TASKS) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        int gk = key0 + vkg * 4 + e;
+        const int gk = key0 + vkg * 4 + e;
+        // Tail rows must be zero: a zero probability times a stale value
+        // could still be NaN.
         rv[e] = gk < a.S ? *(const uint4*)(seg_row<T>(a.v, b, gk) + col0 + vdc * 8) : make_uint4(0, 0, 0, 0);
       }
     }
@@ -121,22 +116,25 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
   auto store_kv = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < K_PER; i++) {
-      int id = tid + i * 256;
-      int key = id / KCH, c = id % KCH;
+      const int id = tid + i * 256;
+      const int key = id / KCH, c = id % KCH;
       *(uint4*)&Ks[buf][key * D + ((c ^ (key & KMASK)) << 3)] = rk[i];
     }
-    if (vtask < V_TASKS) {
-      const uint16_t* v0 = (const uint16_t*)&rv[0];
-      const uint16_t* v1 = (const uint16_t*)&rv[1];
-      const uint16_t* v2 = (const uint16_t*)&rv[2];
-      const uint16_t* v3 = (const uint16_t*)&rv[3];
+    if (tid < V_TASKS) {
+      const uint32_t* w0 = (const uint32_t*)&rv[0];
+      const uint32_t* w1 = (const uint32_t*)&rv[1];
+      const uint32_t* w2 = (const uint32_t*)&rv[2];
+      const uint32_t* w3 = (const uint32_t*)&rv[3];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        int d = vdc * 8 + e;
-        uint2 g;
-        g.x = uint32_t(v0[e]) | (uint32_t(v1[e]) << 16);
-        g.y = uint32_t(v2[e]) | (uint32_t(v3[e]) << 16);
-        *(uint2*)&Vt[buf][d * BKEY + ((vkg ^ (d & 15)) << 2)] = g;
+      for (int e = 0; e < 4; e++) {
+        // Two d rows per 32-bit word: (d, d+1) of keys 4g..4g+3.
+        const uint32_t lo01 = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100);
+        const uint32_t lo23 = __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100);
+        const uint32_t hi01 = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302);
+        const int d = vdc * 8 + 2 * e;
+        *(uint2*)&Vt[buf][d * BKEY + ((vkg ^ (d & 15)) << 2)] = make_uint2(lo01, lo23);
+        *(uint2*)&Vt[buf][(d + 1) * BKEY + ((vkg ^ ((d + 1) & 15)) << 2)] = make_uint2(hi01, hi23);
       }
     }
   };
@@ -149,8 +147,8 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
   float m_run = -INFINITY, l_part = 0.f;
   const float sl = a.scale * kLog2e;
   const float mask_add = -10000.0f * kLog2e;
-  int key_len = a.S;
-  if (a.mask_kind == NDX_MASK_KEY_LENGTH) key_len = a.mask[0];
+  const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
+  const int qm = min(qi, a.T - 1);
 
   const int KB = (a.S + BKEY - 1) / BKEY;
   load_kv(0);
@@ -174,44 +172,50 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
         sacc[t] = AMfma<T>::mma(kf, qf[s], sacc[t]);
       }
     }
-    // Scale, mask, running max.
+    // Scale (into log2 units), mask, running max. The key tail is only
+    // checked in the last block.
+    const bool tail = (kb + 1) * BKEY > a.S;
     float mloc = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int key = kb * BKEY + t * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         float x = sacc[t][r] * sl;
-        if (key >= a.S) {
-          x = -INFINITY;
-        } else if (a.mask_kind == NDX_MASK_KEY_LENGTH) {
+        const int key = kb * BKEY + t * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (MASK == NDX_MASK_KEY_LENGTH) {
           if (key >= key_len) x += mask_add;
-        } else if (a.mask_kind == NDX_MASK_BOOLEAN && qi < a.T) {
-          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qi) * a.mask_stride[2] +
-                             int64_t(key) * a.mask_stride[3];
+        } else if (MASK == NDX_MASK_BOOLEAN) {
+          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
+                             int64_t(min(key, a.S - 1)) * a.mask_stride[3];
           if (a.mask[mi] == 0) x += mask_add;
         }
+        if (tail && key >= a.S) x = -INFINITY;
         sacc[t][r] = x;
         mloc = fmaxf(mloc, x);
       }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     const float m_new = fmaxf(m_run, mloc);
-    const float alpha = exp2f(m_run - m_new);
+    // Rescale the running output only when some lane's max moved: after
+    // the first blocks the maxima settle and the multiply is skipped.
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+      const float alpha = exp2f(m_run - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+    }
     m_run = m_new;
     float psum = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        float p = exp2f(sacc[t][r] - m_new);
+        const float p = exp2f(sacc[t][r] - m_new);
         sacc[t][r] = p;
         psum += p;
       }
-    l_part = l_part * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+    l_part += psum;
 
     // O^T += V^T P^T over four 16-key steps.
 #pragma unroll
@@ -223,12 +227,10 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a, int grid) {
       for (int t = 0; t < DT; t++) {
         const int d = t * 32 + lq;
         const int g1 = 4 * u + lh, g2 = 4 * u + 2 + lh;
-        uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
-        uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
-        V vf;
-        uint4 packed = make_uint4(x1.x, x1.y, x2.x, x2.y);
-        vf = *(const V*)&packed;
-        o[t] = AMfma<T>::mma(vf, pb, o[t]);
+        const uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
+        const uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
+        const uint4 packed = make_uint4(x1.x, x1.y, x2.x, x2.y);
+        o[t] = AMfma<T>::mma(__builtin_bit_cast(V, packed), pb, o[t]);
       }
     }
     if (kb + 1 < KB) store_kv(cur ^ 1);
@@ -359,13 +361,23 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
   if (mfma) {
     int qblocks = (a.T + 127) / 128;
     int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
-    if (a.dtype == NDX_BF16) {
-      if (a.d == 128) hipLaunchKernelGGL((flash_attn_kernel<__bf16, 128>), dim3(grid), dim3(256), 0, s, a, grid);
-      else hipLaunchKernelGGL((flash_attn_kernel<__bf16, 64>), dim3(grid), dim3(256), 0, s, a, grid);
+    const bool bf = a.dtype == NDX_BF16;
+#define NDX_FA(TYPE, DIM, MK) hipLaunchKernelGGL((flash_attn_kernel<TYPE, DIM, MK>), dim3(grid), dim3(256), 0, s, a, grid)
+#define NDX_FA_MASKS(TYPE, DIM)                                  \
+  do {                                                           \
+    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA(TYPE, DIM, 1); \
+    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA(TYPE, DIM, 2); \
+    else NDX_FA(TYPE, DIM, 0);                                   \
+  } while (0)
+    if (bf) {
+      if (a.d == 128) NDX_FA_MASKS(__bf16, 128);
+      else NDX_FA_MASKS(__bf16, 64);
     } else {
-      if (a.d == 128) hipLaunchKernelGGL((flash_attn_kernel<_Float16, 128>), dim3(grid), dim3(256), 0, s, a, grid);
-      else hipLaunchKernelGGL((flash_attn_kernel<_Float16, 64>), dim3(grid), dim3(256), 0, s, a, grid);
+      if (a.d == 128) NDX_FA_MASKS(_Float16, 128);
+      else NDX_FA_MASKS(_Float16, 64);
     }
+#undef NDX_FA_MASKS
+#undef NDX_FA
     return;
   }
   size_t lds = (size_t(GQ) * a.d + size_t(GK) * (a.d + 1) + size_t(GK) * a.dv + size_t(GQ) * GK) * sizeof(float);

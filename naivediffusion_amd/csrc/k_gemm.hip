@@ -83,8 +83,121 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t b, int r
   store_f(a.c, a.c_dtype, b * a.batch_c + int64_t(row) * a.ldc + col, v);
 }
 
+// The epilogue of four consecutive outputs (row, col..col+3): bias,
+// activation or (gated) residual, then one 8- or 16-byte store when the
+// row is aligned for it.
+__device__ __forceinline__ void epilogue_four(const GemmArgs& a, int64_t b, int row, int col, float4 acc,
+                                              bool vec_ok) {
+  if (row >= a.M || col >= a.N) return;
+  float v[4] = {acc.x, acc.y, acc.z, acc.w};
+  const bool full = col + 3 < a.N;
+  if (a.bias) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (full || col + e < a.N) v[e] += load_f(a.bias, a.bias_dtype, col + e);
+  }
+  const int ep = a.epilogue;
+  if (ep == EPI_GELU_TANH) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = gelu_tanh_f(v[e]);
+  } else if (ep == EPI_GELU) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = gelu_f(v[e]);
+  } else if (ep == EPI_SILU) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = silu_f(v[e]);
+  } else if (ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL) {
+    const int64_t ro = b * a.batch_r + int64_t(row) * a.ldr + col;
+    float r[4], g[4] = {1.f, 1.f, 1.f, 1.f};
+    if (full && vec_ok && a.r_dtype == NDX_F32) {
+      float4 rv = *(const float4*)((const float*)a.resid + ro);
+      r[0] = rv.x; r[1] = rv.y; r[2] = rv.z; r[3] = rv.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) r[e] = (full || col + e < a.N) ? load_f(a.resid, a.r_dtype, ro + e) : 0.f;
+    }
+    if (ep == EPI_GATED_RESIDUAL) {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        g[e] = (full || col + e < a.N) ? load_f(a.gate, a.gate_dtype, b * a.batch_gate + col + e) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = r[e] + g[e] * round_to(v[e], a.a_dtype);
+  }
+  const int64_t co = b * a.batch_c + int64_t(row) * a.ldc + col;
+  if (full && vec_ok) {
+    if (a.c_dtype == NDX_F32) {
+      *(float4*)((float*)a.c + co) = make_float4(v[0], v[1], v[2], v[3]);
+      return;
+    }
+    if (a.c_dtype == NDX_BF16) {
+      __bf16 h[4] = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+      *(uint2*)((__bf16*)a.c + co) = *(const uint2*)h;
+      return;
+    }
+    if (a.c_dtype == NDX_F16) {
+      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+      *(uint2*)((_Float16*)a.c + co) = *(const uint2*)h;
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    if (col + e < a.N) store_f(a.c, a.c_dtype, co + e, v[e]);
+}
+
+// Whether the output (and residual) rows allow 16-byte vector access at
+// every multiple-of-4 column.
+__device__ __forceinline__ bool epilogue_vec_ok(const GemmArgs& a) {
+  const int cs = dtype_size(a.c_dtype);
+  bool ok = (uintptr_t)a.c % 16 == 0 && (a.ldc * cs) % 16 == 0 && (a.batch_c * cs) % 16 == 0;
+  if (a.resid) {
+    const int rs = dtype_size(a.r_dtype);
+    ok = ok && (uintptr_t)a.resid % 16 == 0 && (a.ldr * rs) % 16 == 0 && (a.batch_r * rs) % 16 == 0;
+  }
+  return ok;
+}
+
+// Writes the accumulators of one wave (TM x TN tiles of 32 x 32, the MFMA
+// layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4)
+// through LDS one 32-row slice at a time, so the epilogue walks rows of
+// four consecutive outputs and every global store is a vector. stage must
+// hold 32 x (WN + 4) floats for each wave and be free (the main loop is done).
+template <int TM, int TN, int WN>
+__device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][TN],
+                                                float* stage, int row0, int col0) {
+  constexpr int CS = WN + 4;
+  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
+  const bool vec_ok = epilogue_vec_ok(a);
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[i][j][r];
+    __syncthreads();
+    for (int it = lane; it < 32 * (WN / 4); it += 64) {
+      const int rl = it / (WN / 4), c4 = it % (WN / 4);
+      const float4 v = *(const float4*)&stage[rl * CS + c4 * 4];
+      epilogue_four(a, bidx, row0 + i * 32 + rl, col0 + c4 * 4, v, vec_ok);
+    }
+    __syncthreads();
+  }
+}
+
 // Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile.
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ (r & 7)) << 3); }
+
+// Bounds-checked buffer loads: an offset at or past the resource's size
+// reads zeros, so the tile edges need no branches.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // Word 3 = 0x00020000: raw 32-bit dword access, the gfx9-family setting.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 template <int BM, int BN, int WM, int WN, typename T, bool W_INT8>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmArgs a, int grid) {
@@ -97,9 +210,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   constexpr int B_PER = BN * (BK / B_CHUNK) / NT;
   static_assert(A_PER * NT == BM * (BK / 8), "A tile does not split over the threads");
   static_assert(B_PER * NT == BN * (BK / B_CHUNK), "B tile does not split over the threads");
-
-  __shared__ __attribute__((aligned(16))) T As[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) T Bs[2][BN * BK];
+  // One LDS block holds the double-buffered A and B tiles during the K
+  // loop and the epilogue's staging rows afterwards.
+  constexpr int TILE_BYTES = 2 * (BM + BN) * BK * (int)sizeof(T);
+  constexpr int STAGE_BYTES = (BM / WM) * (BN / WN) * 32 * (WN + 4) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
+  T (*As)[BM * BK] = reinterpret_cast<T (*)[BM * BK]>(smem);
+  T (*Bs)[BN * BK] = reinterpret_cast<T (*)[BN * BK]>(smem + 2 * BM * BK * sizeof(T));
 
   int tm, tn;
   if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
@@ -108,8 +225,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
+  // The A rows of this batch and the whole weight, as bounds-checked
+  // buffers (their byte spans are below 2^31, checked on the host).
   const T* A = (const T*)a.a + bidx * a.batch_a;
-  const char* W = (const char*)a.w + bidx * a.batch_w * (W_INT8 ? 1 : (int)sizeof(T));
+  const __amdgpu_buffer_rsrc_t ra_rsrc =
+      make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * (int64_t)sizeof(T)));
+  const int wes = W_INT8 ? 1 : (int)sizeof(T);
+  const __amdgpu_buffer_rsrc_t rw_rsrc = make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * wes));
+
+  // Per-thread load coordinates are fixed across the K loop; the K offset
+  // is added per tile.
+  uint32_t a_off[A_PER], w_off[B_PER];
+  int a_k[A_PER], w_k[B_PER];
+#pragma unroll
+  for (int i = 0; i < A_PER; i++) {
+    const int id = tid + i * NT, r = id >> 3, c = id & 7;
+    a_k[i] = c * 8;
+    a_off[i] = (m0 + r < a.M) ? (uint32_t)((int64_t(m0 + r) * a.lda + c * 8) * (int64_t)sizeof(T)) : kOutOfRange;
+  }
+#pragma unroll
+  for (int i = 0; i < B_PER; i++) {
+    const int id = tid + i * NT, r = id / (BK / B_CHUNK), c = id % (BK / B_CHUNK);
+    w_k[i] = c * B_CHUNK;
+    w_off[i] = (n0 + r < a.N) ? (uint32_t)((int64_t(n0 + r) * a.ldw + c * B_CHUNK) * wes) : kOutOfRange;
+  }
 
   uint4 ra[A_PER];
   uint4 rb[B_PER];
@@ -119,29 +258,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      int id = tid + i * NT;
-      int r = id >> 3, c = id & 7;
-      int gm = m0 + r, gk = k0 + c * 8;
-      if (gm < a.M && gk < a.K)
-        ra[i] = *(const uint4*)(A + int64_t(gm) * a.lda + gk);
-      else
-        ra[i] = make_uint4(0, 0, 0, 0);
+      const bool in = k0 + a_k[i] < a.K;
+      ra[i] = load16(ra_rsrc, in ? a_off[i] + uint32_t(k0 * (int)sizeof(T)) : kOutOfRange);
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
-      int id = tid + i * NT;
-      int r = id / (BK / B_CHUNK), c = id % (BK / B_CHUNK);
-      int gn = n0 + r, gk = k0 + c * B_CHUNK;
-      if (gn < a.N && gk < a.K) {
-        if (W_INT8) {
-          rb[i] = *(const uint4*)(W + int64_t(gn) * a.ldw + gk);
-          rs[W_INT8 ? i : 0] = scale_at(a.scales, a.s_dtype, int64_t(gn) * a.lds + gk / a.qblock);
-        } else {
-          rb[i] = *(const uint4*)(W + (int64_t(gn) * a.ldw + gk) * (int)sizeof(T));
-        }
-      } else {
-        rb[i] = make_uint4(0, 0, 0, 0);
-        if (W_INT8) rs[W_INT8 ? i : 0] = 0.f;
+      const bool in = k0 + w_k[i] < a.K;
+      rb[i] = load16(rw_rsrc, in ? w_off[i] + uint32_t(k0 * wes) : kOutOfRange);
+      if (W_INT8) {
+        const int id = tid + i * NT, r = id / (BK / 16);
+        const int gn = min(n0 + r, a.N - 1);
+        rs[W_INT8 ? i : 0] = scale_at(a.scales, a.s_dtype, int64_t(gn) * a.lds + (k0 + w_k[i]) / a.qblock);
       }
     }
   };
@@ -209,23 +336,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     __syncthreads();
   }
 
-  // Lane l of a 32x32 result holds column l % 32 and rows
-  // 8 * (r / 4) + 4 * (l / 32) + r % 4 for r = 0..15.
-#pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const int col = n0 + wn * WN + j * 32 + lrow;
-    if (col >= a.N) continue;
-    const float bias = a.bias ? load_f(a.bias, a.bias_dtype, col) : 0.f;
-    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + col) : 0.f;
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        if (row < a.M) epilogue_one(a, bidx, row, col, acc[i][j][r], bias, gate);
-      }
-    }
-  }
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
+  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ---- fp32 -------------------------------------------------------------------
@@ -272,8 +384,11 @@ __device__ __forceinline__ void load_w8(const GemmArgs& a, const char* W, int n,
 // from one 16-byte-pair LDS read per operand.
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
   constexpr int BM = 128, BN = 128, WM = 64, WN = 64, TM = 2, TN = 2;
-  __shared__ __attribute__((aligned(16))) float As[2][BM * BK32];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BN * BK32];
+  constexpr int TILE_BYTES = 2 * (BM + BN) * BK32 * 4;
+  constexpr int STAGE_BYTES = 4 * 32 * (WN + 4) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
+  float (*As)[BM * BK32] = reinterpret_cast<float (*)[BM * BK32]>(smem);
+  float (*Bs)[BN * BK32] = reinterpret_cast<float (*)[BN * BK32]>(smem + 2 * BM * BK32 * 4);
   int tm, tn;
   if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
   const int64_t bidx = blockIdx.y;
@@ -371,20 +486,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
     if (kt + 1 < KT) store_tile(cur ^ 1);
     __syncthreads();
   }
-#pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const int col = n0 + wn * WN + j * 32 + lrow;
-    if (col >= a.N) continue;
-    const float bias = a.bias ? load_f(a.bias, a.bias_dtype, col) : 0.f;
-    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + col) : 0.f;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        if (row < a.M) epilogue_one(a, bidx, row, col, acc[i][j][r], bias, gate);
-      }
-  }
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
+  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ---- GEMV ---------------------------------------------------------------------
@@ -479,12 +582,21 @@ static bool a_aligned(const GemmArgs& a) {
   return (uintptr_t)a.a % 16 == 0 && (a.lda * es) % 16 == 0 && (a.batch_a * es) % 16 == 0;
 }
 
+// The buffer loads address one batch of A and the whole weight with 32-bit
+// byte offsets.
+static bool spans_fit(const GemmArgs& a) {
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t a_span = (int64_t(a.M - 1) * a.lda + a.K) * dtype_size(a.a_dtype);
+  const int64_t w_span = (int64_t(a.N - 1) * a.ldw + a.K) * (a.w_dtype == NDX_I8 ? 1 : dtype_size(a.w_dtype));
+  return a_span < lim && w_span < lim;
+}
+
 static GemmKind choose(const GemmArgs& a) {
   const int MR = a.M;
   if (!w_aligned(a)) return K_GENERIC_LINEAR;
   if (MR <= 4 && int64_t(4) * a.K * 4 <= 65536 && a.K % 8 == 0) return K_GEMV;
-  if (!a_aligned(a)) return K_GENERIC_LINEAR;
-  if (a.w_dtype == NDX_I8 && (uintptr_t)a.w % 16) return K_GENERIC_LINEAR;
+  if (!a_aligned(a) || !spans_fit(a)) return K_GENERIC_LINEAR;
+  if (a.w_dtype == NDX_I8 && ((uintptr_t)a.w % 16 || a.ldw % 16)) return K_GENERIC_LINEAR;
   if ((a.a_dtype == NDX_BF16 || a.a_dtype == NDX_F16) && a.K % 16 == 0) {
     int64_t t256 = int64_t((a.M + 255) / 256) * ((a.N + 255) / 256) * a.batch;
     int64_t t128 = int64_t((a.M + 127) / 128) * ((a.N + 127) / 128) * a.batch;

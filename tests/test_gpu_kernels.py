@@ -73,6 +73,40 @@ def test_linear_against_oracle(device, M, K, N, B, compute):
     assert err <= (BF16_TOL if compute == DT.BFloat16 else F32_TOL)
 
 
+# Every tile configuration of the GEMM dispatch, with the family it must pick.
+TILE_CASES = [
+    (64, 3072, 3072, 1, "gemm_mfma_64x128"),
+    (40, 1024, 650, 1, "gemm_mfma_64x128"),
+    (64, 512, 384, 3, "gemm_mfma_64x128"),
+    (256, 3072, 3072, 1, "gemm_mfma_128x128"),
+    (1536, 3072, 12288, 1, "gemm_mfma_256x256"),
+    (1543, 1024, 8200, 1, "gemm_mfma_256x256"),
+    (3, 3072, 1000, 2, "gemv"),
+]
+
+
+@pytest.mark.parametrize("M,K,N,B,family", TILE_CASES)
+@pytest.mark.parametrize("int8", [False, True])
+def test_linear_tile_configurations(device, M, K, N, B, family, int8):
+    print(f"[gpu] tile case M={M} K={K} N={N} B={B} int8={int8}", flush=True)
+    x = bf(normal("tx", (B, 1, M, K)))
+    w = bf(normal("tw", (N, K), 0.02))
+    b = bf(normal("tb", (N,), 0.02))
+    model = nd.ModelBuilder(device, DT.BFloat16, int8Weights=int8)
+    xin = model.Placeholder([B, 1, M, K])
+    model.Compile([Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b))])
+    model.Compiled.SetProfiling(True)
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16))[0]
+    fams = set(model.Compiled.Profile())
+    wq = w
+    if int8 and w.size >= (1 << 16):
+        q, sc = oracle.quantize(w, N)
+        wq = (q.astype(np.float32).reshape(N, -1, 32) * oracle.f16_bits_to_f32(sc)[:, :, None]).reshape(N, K)
+        family = family.replace("gemm_mfma", "gemm_w8_mfma")
+    assert family in fams, fams
+    assert rel_err(out, oracle.linear(x, wq, b)) <= BF16_TOL
+
+
 @pytest.mark.parametrize("epi", ["gelu_tanh", "gelu", "silu", "gated", "residual"])
 def test_linear_epilogues(device, epi):
     M, K, N = 300, 512, 384
