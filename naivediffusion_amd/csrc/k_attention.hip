@@ -17,6 +17,8 @@
 // attn_generic_kernel: any float type and head size, fp32 arithmetic with
 // expf; the fp32-compute path and the reference for odd shapes.
 
+#include <cstdlib>
+
 #include "k_common.h"
 
 namespace ndx {
@@ -64,10 +66,13 @@ __device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <typename T, int D, int MASK>
-__global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, int grid) {
+// QT query tiles of 32 per wave: every K and V fragment read from LDS feeds
+// QT MFMAs. QT = 1 keeps the register file under 256 (two waves per SIMD);
+// QT = 2 halves the LDS traffic per MFMA at one wave per SIMD.
+template <typename T, int D, int MASK, int QT>
+__global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnArgs a, int grid) {
   typedef typename AMfma<T>::V V;
-  constexpr int BQ = 128, BKEY = 64;
+  constexpr int BQ = 128 * QT, BKEY = 64;
   constexpr int KCH = D / 8;                      // 16-byte chunks per key row
   constexpr int KMASK = (KCH < 16 ? KCH : 16) - 1;
   constexpr int K_PER = BKEY * KCH / 256;         // K chunks per thread
@@ -80,15 +85,18 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, int grid
   if (!attn_tile(blockIdx.x, grid, (a.T + BQ - 1) / BQ, a.H, a.B, qb, head, b)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 31, lh = lane >> 5;
-  const int qi = qb * BQ + wave * 32 + lq;
   const int64_t col0 = int64_t(head) * D;
+  int qi[QT];
+#pragma unroll
+  for (int t = 0; t < QT; t++) qi[t] = qb * BQ + (wave * QT + t) * 32 + lq;
 
   // Q^T fragments, resident for the whole key loop.
-  V qf[D / 16];
-  {
-    const T* qrow = seg_row<T>(a.q, b, min(qi, a.T - 1)) + col0;
+  V qf[QT][D / 16];
 #pragma unroll
-    for (int s = 0; s < D / 16; s++) qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
+  for (int t = 0; t < QT; t++) {
+    const T* qrow = seg_row<T>(a.q, b, min(qi[t], a.T - 1)) + col0;
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) qf[t][s] = *(const V*)(qrow + s * 16 + lh * 8);
   }
 
   uint4 rk[K_PER];
@@ -139,16 +147,22 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, int grid
     }
   };
 
-  f32x16 o[DT];
+  f32x16 o[QT][DT];
 #pragma unroll
-  for (int t = 0; t < DT; t++)
+  for (int t = 0; t < QT; t++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) o[t][r] = 0.f;
-  float m_run = -INFINITY, l_part = 0.f;
+    for (int j = 0; j < DT; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[t][j][r] = 0.f;
+  float m_run[QT], l_part[QT];
+#pragma unroll
+  for (int t = 0; t < QT; t++) {
+    m_run[t] = -INFINITY;
+    l_part[t] = 0.f;
+  }
   const float sl = a.scale * kLog2e;
   const float mask_add = -10000.0f * kLog2e;
   const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
-  const int qm = min(qi, a.T - 1);
 
   const int KB = (a.S + BKEY - 1) / BKEY;
   load_kv(0);
@@ -158,99 +172,114 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, int grid
     const int cur = kb & 1;
     if (kb + 1 < KB) load_kv(kb + 1);
 
-    // S^T for 64 keys: two 32-key tiles.
-    f32x16 sacc[2];
+    // S^T for 64 keys: two 32-key tiles per query tile.
+    f32x16 sacc[QT][2];
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
+    for (int t = 0; t < QT; t++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) sacc[t][r] = 0.f;
-      const int key = t * 32 + lq;
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) sacc[t][kt][r] = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+      const int key = kt * 32 + lq;
 #pragma unroll
       for (int s = 0; s < D / 16; s++) {
         const int c = 2 * s + lh;
-        V kf = *(const V*)&Ks[cur][key * D + ((c ^ (key & KMASK)) << 3)];
-        sacc[t] = AMfma<T>::mma(kf, qf[s], sacc[t]);
+        const V kf = *(const V*)&Ks[cur][key * D + ((c ^ (key & KMASK)) << 3)];
+#pragma unroll
+        for (int t = 0; t < QT; t++) sacc[t][kt] = AMfma<T>::mma(kf, qf[t][s], sacc[t][kt]);
       }
     }
     // Scale (into log2 units), mask, running max. The key tail is only
     // checked in the last block.
     const bool tail = (kb + 1) * BKEY > a.S;
-    float mloc = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int t = 0; t < QT; t++) {
+      const int qm = min(qi[t], a.T - 1);
+      float mloc = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float x = sacc[t][r] * sl;
-        const int key = kb * BKEY + t * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (MASK == NDX_MASK_KEY_LENGTH) {
-          if (key >= key_len) x += mask_add;
-        } else if (MASK == NDX_MASK_BOOLEAN) {
-          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
-                             int64_t(min(key, a.S - 1)) * a.mask_stride[3];
-          if (a.mask[mi] == 0) x += mask_add;
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float x = sacc[t][kt][r] * sl;
+          const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (MASK == NDX_MASK_KEY_LENGTH) {
+            if (key >= key_len) x += mask_add;
+          } else if (MASK == NDX_MASK_BOOLEAN) {
+            const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
+                               int64_t(min(key, a.S - 1)) * a.mask_stride[3];
+            if (a.mask[mi] == 0) x += mask_add;
+          }
+          if (tail && key >= a.S) x = -INFINITY;
+          sacc[t][kt][r] = x;
+          mloc = fmaxf(mloc, x);
         }
-        if (tail && key >= a.S) x = -INFINITY;
-        sacc[t][r] = x;
-        mloc = fmaxf(mloc, x);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run[t], mloc);
+      // Rescale the running output only when some lane's max moved: after
+      // the first blocks the maxima settle and the multiply is skipped.
+      if (__builtin_amdgcn_ballot_w64(m_new > m_run[t])) {
+        const float alpha = exp2f(m_run[t] - m_new);
+        l_part[t] *= alpha;
+#pragma unroll
+        for (int j = 0; j < DT; j++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) o[t][j][r] *= alpha;
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    // Rescale the running output only when some lane's max moved: after
-    // the first blocks the maxima settle and the multiply is skipped.
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
-      const float alpha = exp2f(m_run - m_new);
-      l_part *= alpha;
+      m_run[t] = m_new;
+      float psum = 0.f;
 #pragma unroll
-      for (int t = 0; t < DT; t++)
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+        for (int r = 0; r < 16; r++) {
+          const float p = exp2f(sacc[t][kt][r] - m_new);
+          sacc[t][kt][r] = p;
+          psum += p;
+        }
+      l_part[t] += psum;
     }
-    m_run = m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float p = exp2f(sacc[t][r] - m_new);
-        sacc[t][r] = p;
-        psum += p;
-      }
-    l_part += psum;
 
     // O^T += V^T P^T over four 16-key steps.
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      V pb;
+      V pb[QT];
 #pragma unroll
-      for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
+      for (int t = 0; t < QT; t++)
 #pragma unroll
-      for (int t = 0; t < DT; t++) {
-        const int d = t * 32 + lq;
+        for (int j = 0; j < 8; j++) pb[t][j] = (T)sacc[t][u >> 1][(u & 1) * 8 + j];
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) {
+        const int d = dt * 32 + lq;
         const int g1 = 4 * u + lh, g2 = 4 * u + 2 + lh;
         const uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
         const uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
-        const uint4 packed = make_uint4(x1.x, x1.y, x2.x, x2.y);
-        o[t] = AMfma<T>::mma(__builtin_bit_cast(V, packed), pb, o[t]);
+        const V vf = __builtin_bit_cast(V, make_uint4(x1.x, x1.y, x2.x, x2.y));
+#pragma unroll
+        for (int t = 0; t < QT; t++) o[t][dt] = AMfma<T>::mma(vf, pb[t], o[t][dt]);
       }
     }
     if (kb + 1 < KB) store_kv(cur ^ 1);
     __syncthreads();
   }
 
-  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
-  const float inv = 1.0f / l_tot;
-  if (qi < a.T) {
-    T* orow = (T*)out_row(a, b, qi, sizeof(T)) + col0;
 #pragma unroll
-    for (int t = 0; t < DT; t++)
+  for (int t = 0; t < QT; t++) {
+    const float l_tot = l_part[t] + __shfl_xor(l_part[t], 32, 64);
+    const float inv = 1.0f / l_tot;
+    if (qi[t] < a.T) {
+      T* orow = (T*)out_row(a, b, qi[t], sizeof(T)) + col0;
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d = t * 32 + 8 * g + 4 * lh;
-        T v4[4];
+      for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) v4[e] = (T)(o[t][g * 4 + e] * inv);
-        *(uint2*)(orow + d) = *(const uint2*)v4;
-      }
+        for (int g = 0; g < 4; g++) {
+          const int d = dt * 32 + 8 * g + 4 * lh;
+          T v4[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) v4[e] = (T)(o[t][dt][g * 4 + e] * inv);
+          *(uint2*)(orow + d) = *(const uint2*)v4;
+        }
+    }
   }
 }
 
@@ -359,22 +388,35 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
                     rows_aligned(a.q, 2) && rows_aligned(a.k, 2) && rows_aligned(a.v, 2) &&
                     (uintptr_t)a.out[0] % 16 == 0 && (uintptr_t)a.out[1] % 16 == 0;
   if (mfma) {
-    int qblocks = (a.T + 127) / 128;
-    int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
+    // NDX_ATTN_QT=1|2 pins the query tiles per wave (for sweeps).
+    const char* pin = getenv("NDX_ATTN_QT");
+    int qt = pin ? atoi(pin) : 1;
+    if (qt != 2 || a.d != 128) qt = 1;
+    const int qblocks = (a.T + 128 * qt - 1) / (128 * qt);
+    const int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
     const bool bf = a.dtype == NDX_BF16;
-#define NDX_FA(TYPE, DIM, MK) hipLaunchKernelGGL((flash_attn_kernel<TYPE, DIM, MK>), dim3(grid), dim3(256), 0, s, a, grid)
-#define NDX_FA_MASKS(TYPE, DIM)                                  \
-  do {                                                           \
-    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA(TYPE, DIM, 1); \
-    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA(TYPE, DIM, 2); \
-    else NDX_FA(TYPE, DIM, 0);                                   \
+#define NDX_FA(TYPE, DIM, MK, QT) \
+  hipLaunchKernelGGL((flash_attn_kernel<TYPE, DIM, MK, QT>), dim3(grid), dim3(256), 0, s, a, grid)
+#define NDX_FA_MASKS(TYPE, DIM, QT)                                      \
+  do {                                                                   \
+    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA(TYPE, DIM, 1, QT);    \
+    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA(TYPE, DIM, 2, QT);  \
+    else NDX_FA(TYPE, DIM, 0, QT);                                       \
   } while (0)
     if (bf) {
-      if (a.d == 128) NDX_FA_MASKS(__bf16, 128);
-      else NDX_FA_MASKS(__bf16, 64);
+      if (a.d == 128) {
+        if (qt == 2) NDX_FA_MASKS(__bf16, 128, 2);
+        else NDX_FA_MASKS(__bf16, 128, 1);
+      } else {
+        NDX_FA_MASKS(__bf16, 64, 1);
+      }
     } else {
-      if (a.d == 128) NDX_FA_MASKS(_Float16, 128);
-      else NDX_FA_MASKS(_Float16, 64);
+      if (a.d == 128) {
+        if (qt == 2) NDX_FA_MASKS(_Float16, 128, 2);
+        else NDX_FA_MASKS(_Float16, 128, 1);
+      } else {
+        NDX_FA_MASKS(_Float16, 64, 1);
+      }
     }
 #undef NDX_FA_MASKS
 #undef NDX_FA

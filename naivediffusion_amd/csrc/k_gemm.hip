@@ -17,6 +17,11 @@
 //    weight-bandwidth bound, one wave per output feature group.
 //  - gemm_generic_kernel: DmlOps.Gemm with arbitrary strides and transposes.
 
+#include <string.h>
+
+#include <algorithm>
+#include <cstdlib>
+
 #include "k_common.h"
 
 namespace ndx {
@@ -340,6 +345,141 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
+// The large-tile GEMM with the tile loads going straight to LDS
+// (buffer_load_dwordx4 ... lds): each wave-wide load fills one contiguous
+// kilobyte of LDS, eight 128-byte tile rows, lane l landing at l * 16 bytes.
+// The XOR swizzle is applied on the source side: lane l fetches the K chunk
+// (l % 8) ^ (row % 8) of its row, so the tile lands swizzled and no register
+// or LDS-write instruction is spent on staging. Fragments are double
+// buffered in registers: the LDS reads of step s + 1 are in flight while
+// the MFMAs of step s run.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int BM, int BN, int WM, int WN, typename T>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a, int grid) {
+  typedef typename MfmaOp<T>::V V;
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NW = (BM / WM) * (BN / WN);
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_LOADS = BM / 8 / NW;  // kilobyte loads per wave per tile
+  constexpr int B_LOADS = BN / 8 / NW;
+  static_assert(A_LOADS * 8 * NW == BM && B_LOADS * 8 * NW == BN, "tile rows do not split over the waves");
+  constexpr int TILE_BYTES = 2 * (BM + BN) * BK * (int)sizeof(T);
+  constexpr int STAGE_BYTES = NW * 32 * (WN + 4) * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
+  T (*As)[BM * BK] = reinterpret_cast<T (*)[BM * BK]>(smem);
+  T (*Bs)[BN * BK] = reinterpret_cast<T (*)[BN * BK]>(smem + 2 * BM * BK * sizeof(T));
+
+  int tm, tn;
+  if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
+  const int64_t bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  constexpr int ES = (int)sizeof(T);
+
+  const T* A = (const T*)a.a + bidx * a.batch_a;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * ES));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * ES));
+
+  // Lane l of a kilobyte load: row (l / 8) of its 8-row group, physical
+  // chunk l % 8 holding logical K chunk (l % 8) ^ (row % 8).
+  const int lrow8 = lane >> 3;
+  const int kchunk = (lane & 7) ^ lrow8;
+  uint32_t a_row[A_LOADS], w_row[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; i++) {
+    const int r = (wave * A_LOADS + i) * 8 + lrow8;
+    a_row[i] = m0 + r < a.M ? (uint32_t)(int64_t(m0 + r) * a.lda * ES) : kOutOfRange;
+  }
+#pragma unroll
+  for (int i = 0; i < B_LOADS; i++) {
+    const int r = (wave * B_LOADS + i) * 8 + lrow8;
+    w_row[i] = n0 + r < a.N ? (uint32_t)(int64_t(n0 + r) * a.ldw * ES) : kOutOfRange;
+  }
+
+  auto issue_tile = [&](int kt, int buf) {
+    const int k = kt * BK + kchunk * 8;
+    const bool kin = k < a.K;
+    const uint32_t koff = uint32_t(k * ES);
+#pragma unroll
+    for (int i = 0; i < A_LOADS; i++) {
+      const uint32_t off = (kin && a_row[i] != kOutOfRange) ? a_row[i] + koff : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; i++) {
+      const uint32_t off = (kin && w_row[i] != kOutOfRange) ? w_row[i] + koff : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int KT = (a.K + BK - 1) / BK;
+  issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    // The tile after the last reads zeros (every offset is past K): the
+    // loop body stays one block for the scheduler.
+    issue_tile(kt + 1, cur ^ 1);
+    V af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bs[cur][swz(wn * WN + j * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int s = 0; s < BK / 16; s++) {
+      const int p = s & 1;
+      if (s + 1 < BK / 16) {
+        const int c = 2 * (s + 1) + lhalf;
+#pragma unroll
+        for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, c)];
+#pragma unroll
+        for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bs[cur][swz(wn * WN + j * 32 + lrow, c)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[p][i], bf[p][j], acc[i][j]);
+    }
+    // Schedule: the tile DMA first, then the first step's fragments, then
+    // each step's MFMAs with the next step's LDS reads threaded between
+    // them (one read every TM*TN/(TM+TN) MFMAs).
+    constexpr int NF = TM + TN, NM = TM * TN;
+    __builtin_amdgcn_sched_group_barrier(0x0010, A_LOADS + B_LOADS, 0);
+    __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
+#pragma unroll
+    for (int s = 0; s < BK / 16 - 1; s++) {
+      if (NM >= NF) {
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+          __builtin_amdgcn_sched_group_barrier(0x0008, NM / NF, 0);
+          __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
+  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+}
+
 // ---- fp32 -------------------------------------------------------------------
 
 static constexpr int BK32 = 32;
@@ -568,7 +708,10 @@ void launch_gemm_generic(const GemmGenericArgs& g, hipStream_t s) {
 
 // ---- dispatch -----------------------------------------------------------------
 
-enum GemmKind { K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_F32, K_GENERIC_LINEAR };
+enum GemmKind {
+  K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64, K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64, K_F32,
+  K_GENERIC_LINEAR
+};
 
 // Whether every 16-byte (or 8-byte, int8 GEMV) vector load a kernel makes
 // of the weight / the activation rows is aligned.
@@ -598,11 +741,30 @@ static GemmKind choose(const GemmArgs& a) {
   if (!a_aligned(a) || !spans_fit(a)) return K_GENERIC_LINEAR;
   if (a.w_dtype == NDX_I8 && ((uintptr_t)a.w % 16 || a.ldw % 16)) return K_GENERIC_LINEAR;
   if ((a.a_dtype == NDX_BF16 || a.a_dtype == NDX_F16) && a.K % 16 == 0) {
-    int64_t t256 = int64_t((a.M + 255) / 256) * ((a.N + 255) / 256) * a.batch;
-    int64_t t128 = int64_t((a.M + 127) / 128) * ((a.N + 127) / 128) * a.batch;
-    if (t256 >= 192) return K_MFMA_256;
-    if (t128 >= 160 || a.M > 64) return K_MFMA_128;
-    return K_MFMA_64;
+    // NDX_GEMM_TILE pins the tile (for sweeps and the tests that cover every
+    // variant): 256, 128, 64x128, 64x64 select the register-staged kernels,
+    // the same names with an "lds" suffix the direct-to-LDS ones (16-bit
+    // weights only); read per launch.
+    const char* pin = getenv("NDX_GEMM_TILE");
+    if (pin) {
+      if (!strcmp(pin, "256")) return K_MFMA_256;
+      if (!strcmp(pin, "128")) return K_MFMA_128;
+      if (!strcmp(pin, "64x128")) return K_MFMA_64;
+      if (!strcmp(pin, "64x64")) return K_MFMA_64x64;
+      if (!strcmp(pin, "256lds") && a.w_dtype != NDX_I8) return K_LDS_256;
+      if (!strcmp(pin, "128lds") && a.w_dtype != NDX_I8) return K_LDS_128;
+      if (!strcmp(pin, "64x128lds") && a.w_dtype != NDX_I8) return K_LDS_64x128;
+      if (!strcmp(pin, "64x64lds") && a.w_dtype != NDX_I8) return K_LDS_64x64;
+    }
+    // The largest tile whose count still fills the 256 CUs well, fitted to
+    // a sweep of every tile over the MMDiT's GEMM shapes (rows 128 to
+    // 13778, N 3072/9216/12288, K 3072/12288) on MI355X.
+    auto tiles = [&](int bm, int bn) { return int64_t((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) * a.batch; };
+    const bool i8 = a.w_dtype == NDX_I8;
+    if (tiles(256, 256) >= 240) return i8 ? K_MFMA_256 : K_LDS_256;
+    if (tiles(128, 128) >= 700) return i8 ? K_MFMA_128 : K_LDS_128;
+    if (tiles(64, 128) >= 500) return i8 ? K_MFMA_64 : K_LDS_64x128;
+    return i8 ? K_MFMA_64x64 : K_LDS_64x64;
   }
   if (a.a_dtype == NDX_F32 && a.K % 8 == 0) return K_F32;
   return K_GENERIC_LINEAR;
@@ -615,6 +777,11 @@ const char* gemm_family(const GemmArgs& a) {
     case K_MFMA_256: return i8 ? "gemm_w8_mfma_256x256" : "gemm_mfma_256x256";
     case K_MFMA_128: return i8 ? "gemm_w8_mfma_128x128" : "gemm_mfma_128x128";
     case K_MFMA_64: return i8 ? "gemm_w8_mfma_64x128" : "gemm_mfma_64x128";
+    case K_MFMA_64x64: return i8 ? "gemm_w8_mfma_64x64" : "gemm_mfma_64x64";
+    case K_LDS_256: return "gemm_mfma_lds_256x256";
+    case K_LDS_128: return "gemm_mfma_lds_128x128";
+    case K_LDS_64x128: return "gemm_mfma_lds_64x128";
+    case K_LDS_64x64: return "gemm_mfma_lds_64x64";
     case K_F32: return "gemm_f32_mfma_128x128";
     default: return "gemm_linear_generic";
   }
@@ -657,6 +824,17 @@ static void launch_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
+template <int BM, int BN, int WM, int WN>
+static void launch_mfma_lds(const GemmArgs& a, hipStream_t s) {
+  int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  int grid = (tiles + 7) / 8 * 8;
+  dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
+  if (a.a_dtype == NDX_BF16)
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16>), g, b, 0, s, a, grid);
+  else
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16>), g, b, 0, s, a, grid);
+}
+
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M == 0 || a.N == 0 || a.batch == 0) return;
   switch (choose(a)) {
@@ -671,6 +849,11 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_MFMA_256: launch_mfma<256, 256, 128, 128>(a, s); break;
     case K_MFMA_128: launch_mfma<128, 128, 64, 64>(a, s); break;
     case K_MFMA_64: launch_mfma<64, 128, 32, 64>(a, s); break;
+    case K_MFMA_64x64: launch_mfma<64, 64, 32, 32>(a, s); break;
+    case K_LDS_256: launch_mfma_lds<256, 256, 128, 128>(a, s); break;
+    case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
+    case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
+    case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
     case K_F32: {
       int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
       int grid = (tiles + 7) / 8 * 8;

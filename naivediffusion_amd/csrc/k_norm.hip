@@ -124,10 +124,114 @@ __global__ __launch_bounds__(256) void row_norm_wide_kernel(RowNormArgs a) {
   }
 }
 
+// Four consecutive elements of a row as floats (fp32: 16 bytes, bf16 or
+// f16: 8 bytes); the caller guarantees the alignment.
+__device__ __forceinline__ float4 load4(const void* p, int dt, int64_t i) {
+  if (dt == NDX_F32) return *(const float4*)((const float*)p + i);
+  const uint2 u = *(const uint2*)((const uint16_t*)p + i);
+  if (dt == NDX_BF16)
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+  const _Float16* h = (const _Float16*)&u;
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+__device__ __forceinline__ void store4(void* p, int dt, int64_t i, float4 v) {
+  if (dt == NDX_F32) {
+    *(float4*)((float*)p + i) = v;
+  } else if (dt == NDX_BF16) {
+    __bf16 h[4] = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    *(uint2*)((__bf16*)p + i) = *(const uint2*)h;
+  } else {
+    _Float16 h[4] = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    *(uint2*)((_Float16*)p + i) = *(const uint2*)h;
+  }
+}
+
+// The same three norms with D = 256 * NC: lane l holds the four-element
+// chunks l, l + 64, ... (NC of them), so every access is a 16- or 8-byte
+// vector and the wave reads one contiguous kilobyte per instruction.
+template <int NC>
+__global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t batch = row / a.rows_per_batch;
+  const int64_t xoff = batch * a.batch_x + (row % a.rows_per_batch) * a.ldx;
+  constexpr int D = NC * 256;
+  float4 v[NC];
+#pragma unroll
+  for (int j = 0; j < NC; j++) v[j] = load4(a.x, a.x_dtype, xoff + (j * 64 + lane) * 4);
+  float mean = 0.f;
+  if (a.mode != 2) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    mean = wave_sum(s) * (1.0f / D);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) * (1.0f / D) + a.eps);
+  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  const int64_t yoff = row * a.ldy;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const int c = (j * 64 + lane) * 4;
+    float4 n = make_float4((v[j].x - mean) * rstd, (v[j].y - mean) * rstd, (v[j].z - mean) * rstd,
+                           (v[j].w - mean) * rstd);
+    if (a.mode == 1) {
+      const float4 sc = load4(a.weight, a.w_dtype, woff + c);
+      const float4 sh = a.bias ? load4(a.bias, a.b_dtype, boff + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      n = make_float4(n.x * (1.0f + sc.x) + sh.x, n.y * (1.0f + sc.y) + sh.y, n.z * (1.0f + sc.z) + sh.z,
+                      n.w * (1.0f + sc.w) + sh.w);
+    } else {
+      if (a.weight) {
+        const float4 w = load4(a.weight, a.w_dtype, woff + c);
+        n = make_float4(n.x * w.x, n.y * w.y, n.z * w.z, n.w * w.w);
+      }
+      if (a.bias) {
+        const float4 b = load4(a.bias, a.b_dtype, boff + c);
+        n = make_float4(n.x + b.x, n.y + b.y, n.z + b.z, n.w + b.w);
+      }
+    }
+    store4(a.y, a.y_dtype, yoff + c, n);
+  }
+}
+
+static bool vec_ok(const void* p, int dt, int64_t ld, int64_t batch) {
+  if (!p) return true;
+  const int es = dtype_size(dt);
+  if (dt != NDX_F32 && dt != NDX_BF16 && dt != NDX_F16) return false;
+  const int need = dt == NDX_F32 ? 16 : 8;
+  return (uintptr_t)p % need == 0 && (ld * es) % need == 0 && (batch * es) % need == 0;
+}
+
 void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
   if (a.rows == 0) return;
   int vpt = (a.D + 63) / 64;
   dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
+  const bool vec = a.D % 256 == 0 && a.D <= 4096 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) &&
+                   vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, 0, a.batch_w) &&
+                   vec_ok(a.bias, a.b_dtype, 0, a.batch_b);
+  if (vec) {
+    switch (a.D / 256) {
+      case 1: hipLaunchKernelGGL(row_norm_vec_kernel<1>, grid, block, 0, s, a); return;
+      case 2: hipLaunchKernelGGL(row_norm_vec_kernel<2>, grid, block, 0, s, a); return;
+      case 3: hipLaunchKernelGGL(row_norm_vec_kernel<3>, grid, block, 0, s, a); return;
+      case 4: hipLaunchKernelGGL(row_norm_vec_kernel<4>, grid, block, 0, s, a); return;
+      case 5: hipLaunchKernelGGL(row_norm_vec_kernel<5>, grid, block, 0, s, a); return;
+      case 6: hipLaunchKernelGGL(row_norm_vec_kernel<6>, grid, block, 0, s, a); return;
+      case 8: hipLaunchKernelGGL(row_norm_vec_kernel<8>, grid, block, 0, s, a); return;
+      case 10: hipLaunchKernelGGL(row_norm_vec_kernel<10>, grid, block, 0, s, a); return;
+      case 12: hipLaunchKernelGGL(row_norm_vec_kernel<12>, grid, block, 0, s, a); return;
+      case 16: hipLaunchKernelGGL(row_norm_vec_kernel<16>, grid, block, 0, s, a); return;
+      default: break;
+    }
+  }
   if (vpt <= 4) hipLaunchKernelGGL(row_norm_kernel<4>, grid, block, 0, s, a);
   else if (vpt <= 8) hipLaunchKernelGGL(row_norm_kernel<8>, grid, block, 0, s, a);
   else if (vpt <= 16) hipLaunchKernelGGL(row_norm_kernel<16>, grid, block, 0, s, a);
@@ -188,9 +292,62 @@ __global__ __launch_bounds__(256) void head_norm_rotate_kernel(HeadNormRotateArg
   }
 }
 
+// d = 128: 16 lanes per (token, head); lane i of the group owns the four
+// pairs (4i .. 4i+3, 64 + 4i .. 64 + 4i + 3), read and written as vectors.
+__global__ __launch_bounds__(256) void head_norm_rotate128_kernel(HeadNormRotateArgs a) {
+  const int lane = threadIdx.x & 15;
+  const int64_t item = int64_t(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const int64_t total = int64_t(a.B) * a.T * a.H;
+  if (item >= total) return;
+  const int head = (int)(item % a.H);
+  const int64_t bt = item / a.H;
+  const int t = (int)(bt % a.T);
+  const int64_t b = bt / a.T;
+  const int64_t xo = b * a.batch_x + int64_t(t) * a.ldx + int64_t(head) * 128;
+  const int64_t yo = b * a.batch_y + int64_t(t) * a.ldy + int64_t(head) * 128;
+  const int i = lane * 4;
+  float4 lo = load4(a.x, a.x_dtype, xo + i), hi = load4(a.x, a.x_dtype, xo + 64 + i);
+  float ss = (lo.x * lo.x + lo.y * lo.y) + (lo.z * lo.z + lo.w * lo.w) + (hi.x * hi.x + hi.y * hi.y) +
+             (hi.z * hi.z + hi.w * hi.w);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+  const float r = 1.0f / sqrtf(ss * (1.0f / 128) + a.eps);
+  float4 wl = make_float4(1.f, 1.f, 1.f, 1.f), wh = wl;
+  if (a.weight) {
+    wl = make_float4(load_f(a.weight, a.w_dtype, i), load_f(a.weight, a.w_dtype, i + 1),
+                     load_f(a.weight, a.w_dtype, i + 2), load_f(a.weight, a.w_dtype, i + 3));
+    wh = make_float4(load_f(a.weight, a.w_dtype, 64 + i), load_f(a.weight, a.w_dtype, 65 + i),
+                     load_f(a.weight, a.w_dtype, 66 + i), load_f(a.weight, a.w_dtype, 67 + i));
+  }
+  const int xd = a.x_dtype;
+  float l[4] = {round_to(lo.x * r * wl.x, xd), round_to(lo.y * r * wl.y, xd), round_to(lo.z * r * wl.z, xd),
+                round_to(lo.w * r * wl.w, xd)};
+  float h[4] = {round_to(hi.x * r * wh.x, xd), round_to(hi.y * r * wh.y, xd), round_to(hi.z * r * wh.z, xd),
+                round_to(hi.w * r * wh.w, xd)};
+  if (a.cos) {
+    const float4 c = *(const float4*)(a.cos + int64_t(t) * 64 + i);
+    const float4 sn = *(const float4*)(a.sin + int64_t(t) * 64 + i);
+    const float cc[4] = {c.x, c.y, c.z, c.w}, sv[4] = {sn.x, sn.y, sn.z, sn.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float nl = l[e] * cc[e] - h[e] * sv[e];
+      const float nh = h[e] * cc[e] + l[e] * sv[e];
+      l[e] = nl;
+      h[e] = nh;
+    }
+  }
+  store4(a.y, a.y_dtype, yo + i, make_float4(l[0], l[1], l[2], l[3]));
+  store4(a.y, a.y_dtype, yo + 64 + i, make_float4(h[0], h[1], h[2], h[3]));
+}
+
 void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s) {
   int64_t total = int64_t(a.B) * a.T * a.H;
   if (total == 0) return;
+  if (a.d == 128 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) && vec_ok(a.y, a.y_dtype, a.ldy, a.batch_y) &&
+      (!a.cos || ((uintptr_t)a.cos % 16 == 0 && (uintptr_t)a.sin % 16 == 0))) {
+    hipLaunchKernelGGL(head_norm_rotate128_kernel, dim3((unsigned)((total + 15) / 16)), dim3(256), 0, s, a);
+    return;
+  }
   hipLaunchKernelGGL(head_norm_rotate_kernel, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, s, a);
 }
 

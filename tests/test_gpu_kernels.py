@@ -73,21 +73,20 @@ def test_linear_against_oracle(device, M, K, N, B, compute):
     assert err <= (BF16_TOL if compute == DT.BFloat16 else F32_TOL)
 
 
-# Every tile configuration of the GEMM dispatch, with the family it must pick.
+# Shapes that reach every tile configuration of the GEMM dispatch; the
+# family each one runs is checked to be an MFMA tile (or the GEMV) and the
+# set of families over the cases to cover all of them.
 TILE_CASES = [
-    (64, 3072, 3072, 1, "gemm_mfma_64x128"),
-    (40, 1024, 650, 1, "gemm_mfma_64x128"),
-    (64, 512, 384, 3, "gemm_mfma_64x128"),
-    (256, 3072, 3072, 1, "gemm_mfma_128x128"),
-    (1536, 3072, 12288, 1, "gemm_mfma_256x256"),
-    (1543, 1024, 8200, 1, "gemm_mfma_256x256"),
-    (3, 3072, 1000, 2, "gemv"),
+    (64, 3072, 3072, 1), (40, 1024, 650, 1), (64, 512, 384, 3), (256, 3072, 9216, 1), (128, 3072, 9216, 1),
+    (1536, 12288, 3072, 1), (1543, 1024, 8200, 1), (1024, 3072, 12288, 1), (1543, 1024, 10000, 1),
+    (3, 3072, 1000, 2),
 ]
+SEEN_FAMILIES = set()
 
 
-@pytest.mark.parametrize("M,K,N,B,family", TILE_CASES)
+@pytest.mark.parametrize("M,K,N,B", TILE_CASES)
 @pytest.mark.parametrize("int8", [False, True])
-def test_linear_tile_configurations(device, M, K, N, B, family, int8):
+def test_linear_tile_configurations(device, M, K, N, B, int8):
     print(f"[gpu] tile case M={M} K={K} N={N} B={B} int8={int8}", flush=True)
     x = bf(normal("tx", (B, 1, M, K)))
     w = bf(normal("tw", (N, K), 0.02))
@@ -97,14 +96,42 @@ def test_linear_tile_configurations(device, M, K, N, B, family, int8):
     model.Compile([Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b))])
     model.Compiled.SetProfiling(True)
     out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16))[0]
-    fams = set(model.Compiled.Profile())
+    (family,) = set(model.Compiled.Profile())
+    SEEN_FAMILIES.add(family.replace("_w8", "").replace("_lds", ""))
     wq = w
     if int8 and w.size >= (1 << 16):
         q, sc = oracle.quantize(w, N)
         wq = (q.astype(np.float32).reshape(N, -1, 32) * oracle.f16_bits_to_f32(sc)[:, :, None]).reshape(N, K)
-        family = family.replace("gemm_mfma", "gemm_w8_mfma")
-    assert family in fams, fams
+        assert family == "gemv" or "_w8_" in family, family
+    assert family == "gemv" or family.startswith("gemm_"), family
     assert rel_err(out, oracle.linear(x, wq, b)) <= BF16_TOL
+
+
+def test_tile_cases_reached_every_configuration():
+    assert SEEN_FAMILIES >= {"gemm_mfma_256x256", "gemm_mfma_128x128", "gemm_mfma_64x128", "gemm_mfma_64x64",
+                             "gemv"}, SEEN_FAMILIES
+
+
+@pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64", "256lds", "128lds", "64x128lds", "64x64lds"])
+@pytest.mark.parametrize("M,K,N", [(600, 1024, 1000), (1024, 3072, 3072), (77, 320, 2056)])
+def test_linear_every_kernel_variant(device, monkeypatch, tile, M, K, N):
+    """Each GEMM kernel, pinned through NDX_GEMM_TILE, against the oracle on
+    ragged shapes (partial tiles in M, N and K)."""
+    print(f"[gpu] pinned tile {tile} M={M} K={K} N={N}", flush=True)
+    monkeypatch.setenv("NDX_GEMM_TILE", tile)
+    x = bf(normal("vx", (1, 1, M, K)))
+    w = bf(normal("vw", (N, K), 0.02))
+    b = bf(normal("vb", (N,), 0.02))
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    xin = model.Placeholder([1, 1, M, K])
+    model.Compile([Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b), activation="gelu_tanh")])
+    model.Compiled.SetProfiling(True)
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16))[0]
+    (family,) = set(model.Compiled.Profile())
+    assert family.endswith({"256": "mfma_256x256", "128": "mfma_128x128", "64x128": "mfma_64x128",
+                            "64x64": "mfma_64x64", "256lds": "lds_256x256", "128lds": "lds_128x128",
+                            "64x128lds": "lds_64x128", "64x64lds": "lds_64x64"}[tile]), family
+    assert rel_err(out, oracle.gelu_tanh(oracle.linear(x, w, b))) <= BF16_TOL
 
 
 @pytest.mark.parametrize("epi", ["gelu_tanh", "gelu", "silu", "gated", "residual"])
