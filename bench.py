@@ -9,6 +9,11 @@ baseline (the oracle's restatement of the reference's C# CPU layer path,
 timed on this host over one block of the same step and scaled to 60 blocks).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--no-cpu-baseline]
+    python bench.py --calibrate-copy    # a plain 1 GiB device copy, for scaling HBM counters
+
+The roofline's `traffic` (HBM bytes per launch of the dominant kernel) is
+read from the committed rocprofv3 counter summary for that kernel under
+profiles/ (a `bytes_per_launch:` line), null when there is none.
 """
 
 from __future__ import annotations
@@ -31,6 +36,38 @@ HBM_PEAK_GBS = 8000.0
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def calibrate_copy(reps=5):
+    """A plain copy kernel of known size: the library's elementwise identity
+    over a 1 GiB bf16 tensor (reads 1 GiB, writes 1 GiB per launch). The
+    FETCH_SIZE and WRITE_SIZE counters of these launches give the factor
+    that turns those counters into bytes."""
+    import naivediffusion_amd as nd
+    from naivediffusion_amd.graph import Ops
+    from naivediffusion_amd.tensors import HostDataType as DT
+
+    dev = nd.Device()
+    shape = [1, 1, 16384, 32768]
+    g = nd.Graph(dev)
+    x = g.Input(DT.BFloat16, shape)
+    model = nd.CompiledModel(g, [Ops.Identity(x)], dev)
+    src = dev.Normal(DT.BFloat16, shape, 1)
+    dst = dev.Empty(DT.BFloat16, shape)
+    for _ in range(reps):
+        model.DispatchInto([src], [dst])
+    dev.Synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read_per_launch": 2 << 29, "bytes_written_per_launch": 2 << 29,
+                      "launches": reps}), flush=True)
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from its committed counter summary."""
+    for path in sorted((ROOT / "profiles").glob(f"{kernel}_*traffic*.md")):
+        for line in path.read_text().splitlines():
+            if line.strip().startswith("bytes_per_launch:"):
+                return float(line.split(":", 1)[1].split()[0]), path.name
+    return None, None
 
 
 def cpu_baseline(device, cfg, seed, ni, nt):
@@ -91,8 +128,7 @@ def main():
     ap.add_argument("--int8", action="store_true", help="int8 block-quantised weights (bf16 compute)")
     ap.add_argument("--blocks", type=int, default=60)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-steps", type=int, default=None,
-                    help="kernel-timed steps (default: the timed steps themselves)")
+    ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -100,6 +136,10 @@ def main():
         print(f"bench.py runs on one GPU: --gpus {args.gpus} (WORLD_SIZE {world}) is not supported; "
               "the multi-GPU sharding of this path is a design note, not a build.", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import naivediffusion_amd as nd
     from naivediffusion_amd import mmdit, rng
@@ -163,6 +203,7 @@ def main():
     per_launch_flops = dom["flops"] / dom["launches"]
     avg_ms = dom["ms"] / dom["launches"]
     achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
+    traffic, traffic_src = read_traffic(dom_name)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -206,7 +247,10 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_unit": "bytes/launch",
+            "traffic_source": traffic_src,
+            "algorithmic_flop_per_launch": per_launch_flops,
             "launches_per_step": dom["launches"] // args.steps,
             "avg_launch_ms": avg_ms,
         },

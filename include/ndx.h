@@ -279,13 +279,18 @@ NDX_API ndx_status ndx_op_conv2d(ndx_graph* graph, ndx_value x, ndx_value w, ndx
 /* Layers.UpsampleNearest, Graph/Layers.cs:234-235 (DmlOps.Upsample2D). */
 NDX_API ndx_status ndx_op_upsample_nearest(ndx_graph* graph, ndx_value x, int32_t scale,
                                            ndx_value* out);
-/* The 2x2 patch embedding layout of the MMDiT stack (Models/QwenImage/
- * QwenImageDit.cs:243-270 with patch 2): [1, C, H, W] -> [1, 1, (H/p)(W/p),
- * C*p*p], feature order (c, dy, dx); and its inverse. */
-NDX_API ndx_status ndx_op_patchify(ndx_graph* graph, ndx_value x, int32_t patch, ndx_value* out);
+/* The patch layouts of the DiTs' embed and unembed, on the device:
+ * [B, C, H, W] -> [B, 1, (H/p)(W/p), C*p*p] and back. Feature order
+ * NDX_PATCH_CHANNEL_FIRST is (c, dy, dx): AnimaDit.Patchify (Models/Anima/
+ * AnimaDit.cs:193-219) and the MMDiT's 2x2 embed; NDX_PATCH_CHANNEL_LAST is
+ * (dy, dx, c): AnimaDit.Unpatchify (:223-247). */
+#define NDX_PATCH_CHANNEL_FIRST 0
+#define NDX_PATCH_CHANNEL_LAST 1
+NDX_API ndx_status ndx_op_patchify(ndx_graph* graph, ndx_value x, int32_t patch, int32_t order,
+                                   ndx_value* out);
 NDX_API ndx_status ndx_op_unpatchify(ndx_graph* graph, ndx_value x, int32_t patch,
                                      int32_t channels, int32_t height, int32_t width,
-                                     ndx_value* out);
+                                     int32_t order, ndx_value* out);
 
 /* ---- compile / run (Dml/DmlCompiledModel.cs, ModelBuilder.Compile/Run) --- */
 /* DmlGraph.Compile + DmlCompiledModel.Initialize, Dml/DmlGraph.cs:58-163,

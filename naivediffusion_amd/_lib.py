@@ -103,8 +103,8 @@ SIGNATURES = [
     ("ndx_op_group_norm", i32, [vp, i32, i32, i32, i32, f32, i32, P(i32)]),
     ("ndx_op_conv2d", i32, [vp, i32, i32, i32, i32, i32, i32, i32, P(i32)]),
     ("ndx_op_upsample_nearest", i32, [vp, i32, i32, P(i32)]),
-    ("ndx_op_patchify", i32, [vp, i32, i32, P(i32)]),
-    ("ndx_op_unpatchify", i32, [vp, i32, i32, i32, i32, i32, P(i32)]),
+    ("ndx_op_patchify", i32, [vp, i32, i32, i32, P(i32)]),
+    ("ndx_op_unpatchify", i32, [vp, i32, i32, i32, i32, i32, i32, P(i32)]),
     ("ndx_graph_compile", i32, [vp, P(i32), i32, P(vp)]),
     ("ndx_model_sizes", i32, [vp, P(u64), P(u64)]),
     ("ndx_model_counts", i32, [vp, P(i32), P(i32), P(i32)]),

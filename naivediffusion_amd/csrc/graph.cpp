@@ -28,6 +28,9 @@ enum ValueKind { VK_INPUT, VK_CONST, VK_NODE, VK_VIEW };
 
 struct ConstStore {
   std::vector<ndx_tensor*> tensors;
+  // Convolution filters reordered to [Cout, kh, kw, Cin] for the implicit
+  // GEMM, by original tensor; made once, at the first compile that needs it.
+  std::map<const ndx_tensor*, ndx_tensor*> nhwc_filters;
   ~ConstStore() {
     for (auto* t : tensors) free_tensor(t);
   }
@@ -51,7 +54,8 @@ struct GValue {
 
 enum OpKind {
   OP_ELEM, OP_JOIN, OP_LINEAR, OP_GEMM, OP_ATTN, OP_HNR, OP_ROWNORM, OP_GROUPNORM, OP_CONV,
-  OP_UPSAMPLE, OP_PATCH
+  OP_UPSAMPLE, OP_PATCH,
+  OP_NHWC,  // compile-time only: an NCHW value copied to NHWC for the implicit-GEMM convolution
 };
 
 struct GNode {
@@ -938,7 +942,7 @@ NDX_API ndx_status ndx_op_upsample_nearest(ndx_graph* g, ndx_value x, int32_t sc
   NDX_CATCH
 }
 
-NDX_API ndx_status ndx_op_patchify(ndx_graph* g, ndx_value x, int32_t patch, ndx_value* out) {
+NDX_API ndx_status ndx_op_patchify(ndx_graph* g, ndx_value x, int32_t patch, int32_t order, ndx_value* out) {
   NDX_TRY
   NEED(g);
   NEED(out);
@@ -946,11 +950,13 @@ NDX_API ndx_status ndx_op_patchify(ndx_graph* g, ndx_value x, int32_t patch, ndx
   require_float(vx, "the latent");
   int64_t C = vx.v.size[1], H = vx.v.size[2], W = vx.v.size[3];
   if (patch < 1 || H % patch || W % patch) fail(NDX_INVALID_ARG, "the latent does not divide into patches");
+  if (order != NDX_PATCH_CHANNEL_FIRST && order != NDX_PATCH_CHANNEL_LAST) fail(NDX_INVALID_ARG, "bad patch order");
   GNode n;
   n.op = OP_PATCH;
   n.in = {x};
   n.i0 = patch;
   n.i1 = 0;
+  n.i5 = order;
   n.i2 = (int)C;
   n.i3 = (int)H;
   n.i4 = (int)W;
@@ -960,7 +966,7 @@ NDX_API ndx_status ndx_op_patchify(ndx_graph* g, ndx_value x, int32_t patch, ndx
 }
 
 NDX_API ndx_status ndx_op_unpatchify(ndx_graph* g, ndx_value x, int32_t patch, int32_t channels, int32_t height,
-                                     int32_t width, ndx_value* out) {
+                                     int32_t width, int32_t order, ndx_value* out) {
   NDX_TRY
   NEED(g);
   NEED(out);
@@ -970,11 +976,13 @@ NDX_API ndx_status ndx_op_unpatchify(ndx_graph* g, ndx_value x, int32_t patch, i
   if (vx.v.size[1] != 1 || vx.v.size[2] != int64_t(height / patch) * (width / patch) ||
       vx.v.size[3] != int64_t(channels) * patch * patch)
     fail(NDX_INVALID_ARG, "the tokens do not fill the latent");
+  if (order != NDX_PATCH_CHANNEL_FIRST && order != NDX_PATCH_CHANNEL_LAST) fail(NDX_INVALID_ARG, "bad patch order");
   GNode n;
   n.op = OP_PATCH;
   n.in = {x};
   n.i0 = patch;
   n.i1 = 1;
+  n.i5 = order;
   n.i2 = channels;
   n.i3 = height;
   n.i4 = width;
@@ -1002,6 +1010,32 @@ struct Compiler {
     v.v = packed4(s);
     v.kind = VK_NODE;
     v.buffer_elems = numel4(v.v);
+    values.push_back(v);
+    int id = (int)values.size() - 1;
+    values[id].base = id;
+    return id;
+  }
+
+  // The filter value `wid` (a packed constant [Cout, Cin, kh, kw]) reordered
+  // to [Cout, kh, kw, Cin] on the device, as a new constant value.
+  int reordered_filter(int wid) {
+    const GValue& w = values[wid];
+    ndx_tensor* src = w.data;
+    ndx_tensor* r;
+    auto it = g->consts->nhwc_filters.find(src);
+    if (it != g->consts->nhwc_filters.end()) {
+      r = it->second;
+    } else {
+      r = new_tensor(g->dev, w.dtype, src->shape, src->rank);
+      g->consts->tensors.push_back(r);
+      g->consts->nhwc_filters[src] = r;
+      launch_reorder_filter(src->ptr, r->ptr, w.dtype, w.v.size[0], w.v.size[1], w.v.size[2] * w.v.size[3],
+                            g->dev->stream);
+      hip_check(hipGetLastError(), "filter reorder launch");
+      hip_check(hipStreamSynchronize(g->dev->stream), "filter reorder");
+    }
+    GValue v = w;
+    v.data = r;
     values.push_back(v);
     int id = (int)values.size() - 1;
     values[id].base = id;
@@ -1063,10 +1097,27 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
       const GValue& o = V[n.out];
       const GValue& x = V[n.in[0]];
       n.flops = 2.0 * numel4(o.v) * x.v.size[1] * n.i3 * n.i4;
-      n.bytes = bytes_of(n.in[0]) + bytes_of(n.in[1]) + out_b;
+      n.bytes = bytes_of(n.in[0]) + bytes_of(n.in[1]) + out_b + bytes_of(n.in[2]) + bytes_of(n.in[3]);
       n.family = std::string("conv2d_") + dtype_name(x.dtype);
+      if (n.i5) {
+        ConvArgs a{};
+        a.N = (int)x.v.size[0];
+        a.Cin = (int)x.v.size[1];
+        a.H = (int)x.v.size[2];
+        a.W = (int)x.v.size[3];
+        a.Cout = (int)o.v.size[1];
+        a.kh = n.i3;
+        a.kw = n.i4;
+        a.Ho = (int)o.v.size[2];
+        a.Wo = (int)o.v.size[3];
+        n.family = conv_family(a);
+      }
       break;
     }
+    case OP_NHWC:
+      n.bytes = 2 * out_b;
+      n.family = "nchw_to_nhwc";
+      break;
     default: {
       double b = out_b;
       for (int id : n.in) b += bytes_of(id);
@@ -1201,11 +1252,33 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
             n.in[j] = c.pack(n.in[j], sched);
         break;
       case OP_GROUPNORM:
-      case OP_CONV:
       case OP_PATCH:
         for (auto& id : n.in)
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
         break;
+      case OP_CONV: {
+        for (auto& id : n.in)
+          if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
+        // 16-bit filters over a multiple of 64 input channels run as an
+        // implicit GEMM: the input copied to NHWC just before, the filter
+        // reordered once.
+        const GValue& x = c.values[n.in[0]];
+        const GValue& w = c.values[n.in[1]];
+        const int64_t lim = int64_t(1) << 31;
+        const bool fits = x.v.size[1] * x.v.size[2] * x.v.size[3] * 2 < lim && numel4(w.v) * 2 < lim;
+        if (!w.quant && w.kind == VK_CONST && w.base == n.in[1] && w.offset == 0 && w.data && fits &&
+            conv_gemm_eligible(x.dtype, w.dtype, (int)x.v.size[1])) {
+          GNode t;
+          t.op = OP_NHWC;
+          t.in = {n.in[0]};
+          t.out = c.new_owner(x.dtype, x.v, 4);
+          sched.push_back(t);
+          n.in[0] = t.out;
+          n.in[1] = c.reordered_filter(n.in[1]);
+          n.i5 = 1;
+        }
+        break;
+      }
       default:
         break;
     }
@@ -1608,7 +1681,14 @@ struct Runner {
         a.pad = n.i1;
         a.Ho = (int)o.v.size[2];
         a.Wo = (int)o.v.size[3];
-        launch_conv2d(a, s);
+        if (n.i5) launch_conv_gemm(a, s);
+        else launch_conv2d(a, s);
+        break;
+      }
+      case OP_NHWC: {
+        const GValue& x = val(n.in[0]);
+        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], x.v.size[1], x.v.size[2] * x.v.size[3],
+                            s);
         break;
       }
       case OP_UPSAMPLE: {
@@ -1634,6 +1714,7 @@ struct Runner {
         a.y_dtype = val(n.out).dtype;
         a.p = n.i0;
         a.inverse = n.i1;
+        a.channel_last = n.i5;
         a.N = (int)val(n.out).v.size[0];
         a.C = n.i2;
         a.H = n.i3;

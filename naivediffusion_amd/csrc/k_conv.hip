@@ -5,7 +5,11 @@
 // optional residual added to the output. Filters may be int8 with block
 // scales along Cin*kh*kw (ModelBuilder.Weight, Graph/ModelBuilder.cs:61-64).
 //
-// Direct form: one thread per output element, fp32 accumulation.
+// Direct form: one thread per output element, fp32 accumulation. The
+// 16-bit convolutions with Cin a multiple of 64 go to the implicit GEMM of
+// k_gemm.hip instead; the layout changes it needs are here.
+
+#include <stdexcept>
 
 #include "k_common.h"
 
@@ -50,6 +54,50 @@ __global__ void conv2d_direct_kernel(ConvArgs a, int64_t total) {
     if (a.resid) acc += load_f(a.resid, a.y_dtype, id);
     store_f(a.y, a.y_dtype, id, acc);
   }
+}
+
+// [n, c, hw] -> [n, hw, c] for 16-bit elements, through a 64 x 64 LDS tile:
+// reads run along hw, writes along c.
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const uint16_t* x, uint16_t* y, int64_t c, int64_t hw) {
+  __shared__ uint16_t tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t c0 = int64_t(blockIdx.y) * 64, p0 = int64_t(blockIdx.x) * 64;
+  const uint16_t* xb = x + b * c * hw;
+  uint16_t* yb = y + b * c * hw;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t ch = c0 + r, p = p0 + tx;
+    if (ch < c && p < hw) tile[r][tx] = xb[ch * hw + p];
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t p = p0 + r, ch = c0 + tx;
+    if (ch < c && p < hw) yb[p * c + ch] = tile[tx][r];
+  }
+}
+
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s) {
+  if (dtype_size(dtype) != 2) throw std::runtime_error("nchw_to_nhwc: 16-bit elements only");
+  dim3 g((unsigned)((hw + 63) / 64), (unsigned)((c + 63) / 64), (unsigned)n);
+  hipLaunchKernelGGL(nchw_to_nhwc_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, hw);
+}
+
+// Filters [cout, cin, taps] -> [cout, taps, cin] (16-bit elements).
+__global__ void reorder_filter_kernel(const uint16_t* w, uint16_t* y, int64_t cout, int64_t cin, int64_t taps) {
+  const int64_t total = cout * cin * taps;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t ci = i % cin, t = (i / cin) % taps, co = i / (cin * taps);
+    y[i] = w[(co * cin + ci) * taps + t];
+  }
+}
+
+void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
+                           hipStream_t s) {
+  if (dtype_size(dtype) != 2) throw std::runtime_error("reorder_filter: 16-bit elements only");
+  const int64_t total = cout * cin * taps;
+  const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(reorder_filter_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, s, (const uint16_t*)w,
+                     (uint16_t*)y, cout, cin, taps);
 }
 
 void launch_conv2d(const ConvArgs& a, hipStream_t s) {

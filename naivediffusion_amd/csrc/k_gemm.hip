@@ -101,6 +101,11 @@ __device__ __forceinline__ void epilogue_four(const GemmArgs& a, int64_t b, int 
     for (int e = 0; e < 4; e++)
       if (full || col + e < a.N) v[e] += load_f(a.bias, a.bias_dtype, col + e);
   }
+  if (a.row_bias) {
+    const float rb = load_f(a.row_bias, a.row_bias_dtype, row);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] += rb;
+  }
   const int ep = a.epilogue;
   if (ep == EPI_GELU_TANH) {
 #pragma unroll
@@ -355,7 +360,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 // the MFMAs of step s run.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int BM, int BN, int WM, int WN, typename T>
+template <int BM, int BN, int WM, int WN, typename T, bool CONV>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a, int grid) {
   typedef typename MfmaOp<T>::V V;
   constexpr int WAVES_N = BN / WN;
@@ -380,13 +385,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
 
   const T* A = (const T*)a.a + bidx * a.batch_a;
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * ES));
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * ES));
+  const __amdgpu_buffer_rsrc_t rw =
+      CONV ? make_rsrc((const T*)a.w + bidx * a.batch_w, (uint32_t)(int64_t(a.conv_h) * a.conv_w * a.conv_cin * ES))
+           : make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * ES));
 
   // Lane l of a kilobyte load: row (l / 8) of its 8-row group, physical
   // chunk l % 8 holding logical K chunk (l % 8) ^ (row % 8).
   const int lrow8 = lane >> 3;
   const int kchunk = (lane & 7) ^ lrow8;
   uint32_t a_row[A_LOADS], w_row[B_LOADS];
+  int pix_y[CONV ? B_LOADS : 1], pix_x[CONV ? B_LOADS : 1];
 #pragma unroll
   for (int i = 0; i < A_LOADS; i++) {
     const int r = (wave * A_LOADS + i) * 8 + lrow8;
@@ -395,7 +403,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
 #pragma unroll
   for (int i = 0; i < B_LOADS; i++) {
     const int r = (wave * B_LOADS + i) * 8 + lrow8;
-    w_row[i] = n0 + r < a.N ? (uint32_t)(int64_t(n0 + r) * a.ldw * ES) : kOutOfRange;
+    if (CONV) {
+      // Output pixel n0 + r reads input rows oy * stride - pad + ky; a row
+      // past the output puts its taps far outside the image.
+      const int n = n0 + r;
+      const int oy = n / a.conv_wo, ox = n - oy * a.conv_wo;
+      pix_y[i] = n < a.N ? oy * a.conv_stride - a.conv_pad : -(1 << 20);
+      pix_x[i] = ox * a.conv_stride - a.conv_pad;
+    } else {
+      w_row[i] = n0 + r < a.N ? (uint32_t)(int64_t(n0 + r) * a.ldw * ES) : kOutOfRange;
+    }
   }
 
   auto issue_tile = [&](int kt, int buf) {
@@ -407,10 +424,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
       const uint32_t off = (kin && a_row[i] != kOutOfRange) ? a_row[i] + koff : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
     }
+    if (CONV) {
+      // A K tile lies within one tap (Cin is a multiple of BK): (ky, kx)
+      // and the channel offset are uniform over the workgroup.
+      const int k0 = kt * BK;
+      const int tap = k0 / a.conv_cin;
+      const int ci = k0 - tap * a.conv_cin + kchunk * 8;
+      const int ky = tap / a.conv_kw, kx = tap - ky * a.conv_kw;
 #pragma unroll
-    for (int i = 0; i < B_LOADS; i++) {
-      const uint32_t off = (kin && w_row[i] != kOutOfRange) ? w_row[i] + koff : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      for (int i = 0; i < B_LOADS; i++) {
+        const int iy = pix_y[i] + ky, ix = pix_x[i] + kx;
+        const bool in = kin && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
+        const uint32_t off = in ? uint32_t(((iy * a.conv_w + ix) * a.conv_cin + ci) * ES) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_LOADS; i++) {
+        const uint32_t off = (kin && w_row[i] != kOutOfRange) ? w_row[i] + koff : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      }
     }
   };
 
@@ -824,15 +857,80 @@ static void launch_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool CONV = false>
 static void launch_mfma_lds(const GemmArgs& a, hipStream_t s) {
   int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   int grid = (tiles + 7) / 8 * 8;
   dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
   if (a.a_dtype == NDX_BF16)
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16>), g, b, 0, s, a, grid);
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, CONV>), g, b, 0, s, a, grid);
   else
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16>), g, b, 0, s, a, grid);
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, CONV>), g, b, 0, s, a, grid);
+}
+
+// ---- implicit-GEMM convolution ----------------------------------------------
+//
+// y[b, co, p] = sum_k F[co, k] * X_b[p, k] with F the filter reordered to
+// [Cout, kh, kw, Cin] and X_b the implicit im2col of the NHWC input: the
+// output lands in NCHW directly (rows are channels, columns pixels).
+
+bool conv_gemm_eligible(int x_dtype, int w_dtype, int cin) {
+  return (x_dtype == NDX_BF16 || x_dtype == NDX_F16) && w_dtype == x_dtype && cin % BK == 0;
+}
+
+enum ConvKind { CK_256, CK_128, CK_64x128, CK_64x64 };
+
+static ConvKind conv_choose(const GemmArgs& g) {
+  // NDX_CONV_TILE=256|128|64x128|64x64 pins the tile (for sweeps and the
+  // tests that cover every variant); read per launch.
+  if (const char* pin = getenv("NDX_CONV_TILE")) {
+    if (!strcmp(pin, "256")) return CK_256;
+    if (!strcmp(pin, "128")) return CK_128;
+    if (!strcmp(pin, "64x128")) return CK_64x128;
+    if (!strcmp(pin, "64x64")) return CK_64x64;
+  }
+  auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch; };
+  if (g.M >= 256 && tiles(256, 256) >= 240) return CK_256;
+  if (g.M >= 128 && tiles(128, 128) >= 500) return CK_128;
+  if (tiles(64, 128) >= 500) return CK_64x128;
+  return CK_64x64;
+}
+
+static GemmArgs conv_gemm_args(const ConvArgs& c) {
+  GemmArgs g{};
+  const int taps = c.kh * c.kw;
+  g.a = c.w; g.lda = int64_t(taps) * c.Cin; g.batch_a = 0; g.a_dtype = c.x_dtype;
+  g.w = c.x; g.ldw = 0; g.batch_w = int64_t(c.H) * c.W * c.Cin; g.w_dtype = c.x_dtype;
+  g.c = c.y; g.ldc = int64_t(c.Ho) * c.Wo; g.batch_c = int64_t(c.Cout) * c.Ho * c.Wo; g.c_dtype = c.y_dtype;
+  g.row_bias = c.bias; g.row_bias_dtype = c.bias_dtype;
+  if (c.resid) {
+    g.resid = c.resid; g.ldr = g.ldc; g.batch_r = g.batch_c; g.r_dtype = c.y_dtype;
+    g.epilogue = EPI_RESIDUAL;
+  }
+  g.M = c.Cout; g.N = c.Ho * c.Wo; g.K = taps * c.Cin; g.batch = c.N;
+  g.conv_cin = c.Cin; g.conv_h = c.H; g.conv_w = c.W; g.conv_wo = c.Wo; g.conv_kw = c.kw;
+  g.conv_stride = c.stride; g.conv_pad = c.pad;
+  return g;
+}
+
+const char* conv_family(const ConvArgs& c) {
+  switch (conv_choose(conv_gemm_args(c))) {
+    case CK_256: return "conv_mfma_256x256";
+    case CK_128: return "conv_mfma_128x128";
+    case CK_64x128: return "conv_mfma_64x128";
+    default: return "conv_mfma_64x64";
+  }
+}
+
+void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
+  const GemmArgs g = conv_gemm_args(c);
+  if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+  switch (conv_choose(g)) {
+    case CK_256: launch_mfma_lds<256, 256, 128, 128, true>(g, s); break;
+    case CK_128: launch_mfma_lds<128, 128, 64, 64, true>(g, s); break;
+    case CK_64x128: launch_mfma_lds<64, 128, 32, 64, true>(g, s); break;
+    default: launch_mfma_lds<64, 64, 32, 32, true>(g, s); break;
+  }
 }
 
 void launch_gemm(const GemmArgs& a, hipStream_t s) {

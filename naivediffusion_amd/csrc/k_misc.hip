@@ -86,7 +86,8 @@ void launch_upsample(const UpsampleArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(upsample_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
 }
 
-// [N, C, H, W] <-> [N, (H/p)(W/p), C p p] with feature order (c, dy, dx).
+// [N, C, H, W] <-> [N, (H/p)(W/p), C p p] with feature order (c, dy, dx),
+// or (dy, dx, c) when channel_last.
 __global__ void patch_kernel(PatchArgs a, int64_t total) {
   int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   int64_t step = int64_t(gridDim.x) * blockDim.x;
@@ -98,7 +99,16 @@ __global__ void patch_kernel(PatchArgs a, int64_t total) {
     int64_t n = i / per, j = i % per;
     int64_t token = j / feat, f = j % feat;
     int64_t ty = token / wp, tx = token % wp;
-    int64_t c = f / (p * p), dy = (f / p) % p, dx = f % p;
+    int64_t c, dy, dx;
+    if (a.channel_last) {
+      dy = f / (int64_t(p) * a.C);
+      dx = (f / a.C) % p;
+      c = f % a.C;
+    } else {
+      c = f / (p * p);
+      dy = (f / p) % p;
+      dx = f % p;
+    }
     int64_t img = n * per + (c * a.H + ty * p + dy) * a.W + tx * p + dx;
     if (!a.inverse)
       store_f(a.y, a.y_dtype, i, load_f(a.x, a.x_dtype, img));

@@ -70,6 +70,14 @@ struct GemmArgs {
   const void* resid; int64_t ldr; int64_t batch_r; int r_dtype;
   int M, N, K, batch;
   int epilogue;
+  // A per-row term added with the bias (a convolution's per-channel bias,
+  // where rows are output channels).
+  const void* row_bias; int row_bias_dtype;
+  // Implicit-GEMM convolution: with conv_cin > 0 the weight operand's row n
+  // is output pixel n, gathered from an NHWC input [batch, H, W, Cin] (w,
+  // batch_w elements per image) at taps (ky, kx) of a kw-wide filter whose
+  // K index is (ky * kw + kx) * Cin + ci.
+  int conv_cin, conv_h, conv_w, conv_wo, conv_kw, conv_stride, conv_pad;
 };
 
 // DmlOps.Gemm in full generality (any strides, transposes, alpha, beta): a
@@ -167,6 +175,7 @@ struct PatchArgs {
   const void* x; void* y; int x_dtype; int y_dtype;
   int N, C, H, W, p;
   int inverse;
+  int channel_last;  // feature order (dy, dx, c) instead of (c, dy, dx)
 };
 
 // ---- launchers (defined in the k_*.hip files) ---------------------------------
@@ -178,6 +187,15 @@ void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s);
 void launch_row_norm(const RowNormArgs& a, hipStream_t s);
 void launch_group_norm(const GroupNormArgs& a, hipStream_t s);
 void launch_conv2d(const ConvArgs& a, hipStream_t s);
+// The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, Cin]
+// (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types,
+// Cin a multiple of 64.
+bool conv_gemm_eligible(int x_dtype, int w_dtype, int cin);
+void launch_conv_gemm(const ConvArgs& a, hipStream_t s);
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s);
+void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
+                           hipStream_t s);
+const char* conv_family(const ConvArgs& a);
 void launch_elementwise(const ElemArgs& a, hipStream_t s);
 void launch_upsample(const UpsampleArgs& a, hipStream_t s);
 void launch_patch(const PatchArgs& a, hipStream_t s);

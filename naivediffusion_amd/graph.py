@@ -24,6 +24,7 @@ NONE = -1
 UNARY_IDENTITY, UNARY_SIGMOID, UNARY_SILU, UNARY_GELU, UNARY_TANH, UNARY_GELU_TANH = range(6)
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
 EPI_NONE, EPI_GELU_TANH, EPI_GELU, EPI_SILU, EPI_GATED_RESIDUAL, EPI_RESIDUAL = range(6)
+PATCH_CHANNEL_FIRST, PATCH_CHANNEL_LAST = 0, 1  # feature order (c, dy, dx) or (dy, dx, c)
 
 
 class MaskType:
@@ -294,12 +295,13 @@ class Ops:
         return g._new("ndx_op_group_norm", x.id, _id(weight), _id(bias), int(groups), float(epsilon), int(silu))
 
     @staticmethod
-    def Patchify(x, patch):
-        return x.graph._new("ndx_op_patchify", x.id, int(patch))
+    def Patchify(x, patch, order=PATCH_CHANNEL_FIRST):
+        return x.graph._new("ndx_op_patchify", x.id, int(patch), int(order))
 
     @staticmethod
-    def Unpatchify(x, patch, channels, height, width):
-        return x.graph._new("ndx_op_unpatchify", x.id, int(patch), int(channels), int(height), int(width))
+    def Unpatchify(x, patch, channels, height, width, order=PATCH_CHANNEL_FIRST):
+        return x.graph._new("ndx_op_unpatchify", x.id, int(patch), int(channels), int(height), int(width),
+                            int(order))
 
 
 class CompiledModel:

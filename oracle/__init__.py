@@ -75,6 +75,7 @@ def lib():
         L.orc_qwen_rope_tables.argtypes = [c_int, c_int, c_int, c_int, _f32p, _f32p]
         L.orc_mmdit_rope_tables.argtypes = [c_int, c_int, c_int, _f32p, _f32p]
         L.orc_causal_table.argtypes = [c_int, c_int, _i32p]
+        L.orc_anima_rope_tables.argtypes = [c_int, c_int, c_int, _f32p, _f32p]
         L.orc_mmdit_block.argtypes = [vp, c_int, vp, c_int, _f32p, c_int, c_int, c_int, c_int, vp, vp, _f32p, _f32p,
                                       c_int, c_float]
         _lib = L
@@ -327,3 +328,211 @@ def mmdit_block(x_img, x_txt, temb, img: dict, txt: dict, heads, cos, sin, key_l
     lib().orc_mmdit_block(_ptr(xi), xi.shape[0], _ptr(xt), xt.shape[0], t, t.size, D, heads, F,
                           ctypes.byref(si), ctypes.byref(stx), _f32(cos), _f32(sin), key_len, eps)
     return xi, xt
+
+
+# ---- Anima (Models/Anima/AnimaDit.cs) ------------------------------------------------
+
+def anima_rope_tables(rows, cols, head_dim=128):
+    """AnimaDit.RopeTables (oracle.c orc_anima_rope_tables): [rows*cols, head_dim/2]."""
+    c = np.empty((rows * cols, head_dim // 2), np.float32)
+    s = np.empty((rows * cols, head_dim // 2), np.float32)
+    lib().orc_anima_rope_tables(rows, cols, head_dim, c, s)
+    return c, s
+
+
+def anima_patchify(latent, patch=2):
+    """AnimaDit.Patchify, AnimaDit.cs:193-219: [C, H, W] -> [tokens, C*p*p],
+    patch (i, j) feature c*p*p + m*p + n = channel c at (p*i + m, p*j + n)."""
+    x = _f32(latent)
+    C, H, W = x.shape
+    out = np.empty(((H // patch) * (W // patch), C * patch * patch), np.float32)
+    for i in range(H // patch):
+        for j in range(W // patch):
+            for c in range(C):
+                for m in range(patch):
+                    for n in range(patch):
+                        out[i * (W // patch) + j, c * patch * patch + m * patch + n] = x[c, i * patch + m, j * patch + n]
+    return out
+
+
+def anima_unpatchify(tokens, channels, height, width, patch=2):
+    """AnimaDit.Unpatchify, AnimaDit.cs:223-247: feature (p1*p + p2)*C + c is
+    channel c at (p*i + p1, p*j + p2)."""
+    t = _f32(tokens)
+    out = np.empty((channels, height, width), np.float32)
+    cols = width // patch
+    for i in range(height // patch):
+        for j in range(cols):
+            for p1 in range(patch):
+                for p2 in range(patch):
+                    for c in range(channels):
+                        out[c, i * patch + p1, j * patch + p2] = t[i * cols + j, (p1 * patch + p2) * channels + c]
+    return out
+
+
+def anima_modulation(temb, lora, w1, w2, chunks, width):
+    """AnimaDit.Modulation, AnimaDit.cs:270-291: Linear(Linear(SiLU(temb),
+    W1), W2) + the shared term (its first chunks * width entries), cut into
+    `chunks` rows of the model width."""
+    h = silu(_f32(temb).reshape(1, -1))
+    m = linear(linear(h, w1), w2)[0] + _f32(lora).reshape(-1)[: chunks * width]
+    return [m[i * width:(i + 1) * width] for i in range(chunks)]
+
+
+def anima_attention(x, source, w: dict, prefix, heads, cos=None, sin=None, eps=1e-6):
+    """AnimaDit.Attention, AnimaDit.cs:295-323: q, k per-head RMS-normed
+    (rotated when tables are given), v plain, Attend, the output projection.
+    No biases."""
+    D = x.shape[-1]
+    d = D // heads
+    q = linear(x, w[f"{prefix}.q_proj.weight"])
+    k = linear(source, w[f"{prefix}.k_proj.weight"])
+    v = linear(source, w[f"{prefix}.v_proj.weight"])
+    q = rms_norm(q.reshape(-1, d), w[f"{prefix}.q_norm.weight"], eps).reshape(q.shape)
+    k = rms_norm(k.reshape(-1, d), w[f"{prefix}.k_norm.weight"], eps).reshape(k.shape)
+    if cos is not None:
+        q = rope(q, heads, cos, sin)
+        k = rope(k, heads, cos, sin)
+    a = mha(q[None], k[None], v[None], heads)[0]
+    return linear(a, w[f"{prefix}.output_proj.weight"])
+
+
+def anima_block(x, temb, lora, context, w: dict, i, heads, cos, sin, eps=1e-6):
+    """AnimaDit.Block, AnimaDit.cs:325-358, on the fp32 residual x [N, D]:
+    self-attention with rotary positions, cross-attention into the context,
+    exact-GELU MLP, each modulated and gated by its low-rank adaLN."""
+    D = x.shape[-1]
+    p = f"blocks.{i}"
+    x = _f32(x).copy()
+    mods = {}
+    for part in ("self_attn", "cross_attn", "mlp"):
+        q = f"{p}.adaln_modulation_{part}"
+        mods[part] = anima_modulation(temb, lora, w[f"{q}.1.weight"], w[f"{q}.2.weight"], 3, D)
+    sh, sc, g = mods["self_attn"]
+    h = modulate(x, sh, sc, eps)
+    x = x + g * anima_attention(h, h, w, f"{p}.self_attn", heads, cos, sin, eps)
+    sh, sc, g = mods["cross_attn"]
+    h = modulate(x, sh, sc, eps)
+    x = x + g * anima_attention(h, _f32(context), w, f"{p}.cross_attn", heads, None, None, eps)
+    sh, sc, g = mods["mlp"]
+    h = modulate(x, sh, sc, eps)
+    f = gelu(linear(h, w[f"{p}.mlp.layer1.weight"]))
+    return x + g * linear(f, w[f"{p}.mlp.layer2.weight"])
+
+
+def anima_step(latent, sigma, context, w: dict, blocks, heads, eps=1e-6, patch=2):
+    """AnimaDit.Predict + Build, AnimaDit.cs:120-132 and :360-404: patchify,
+    embed (the 16 real channels' columns), the time embedding (RMS-normed
+    sinusoid; the shared adaLN term through t_embedder), the blocks, the
+    final modulated projection, unpatchify. latent [C, H, W] -> flow [C, H, W]."""
+    C, H, W = latent.shape
+    D = w["x_embedder.proj.1.weight"].shape[0]
+    kept = C * patch * patch
+    tokens = anima_patchify(latent, patch)
+    x = linear(tokens, np.ascontiguousarray(w["x_embedder.proj.1.weight"][:, :kept]))
+    time = sinusoid(float(sigma), D).reshape(1, D)
+    temb = rms_norm(time, w["t_embedding_norm.weight"], eps)
+    lora = linear(silu(linear(time, w["t_embedder.1.linear_1.weight"])), w["t_embedder.1.linear_2.weight"])
+    cos, sin = anima_rope_tables(H // patch, W // patch, D // heads)
+    for i in range(blocks):
+        x = anima_block(x, temb, lora, context, w, i, heads, cos, sin, eps)
+    sh, sc = anima_modulation(temb, lora, w["final_layer.adaln_modulation.1.weight"],
+                              w["final_layer.adaln_modulation.2.weight"], 2, D)
+    out = linear(modulate(x, sh, sc, eps), w["final_layer.linear.weight"])
+    return anima_unpatchify(out, C, H, W, patch)
+
+
+# ---- SDXL's UNet (Models/Sdxl/UNetModel.cs, UNetLayers.cs) ----------------------------
+
+def sdxl_resnet(x, silu_temb, w: dict, p: str, groups=32, eps=1e-5):
+    """UNetModel.ResnetBlock, UNetModel.cs:230-254. x [B, C, H, W];
+    silu_temb [B, T] (SiLU of the time embedding)."""
+    x = _f32(x)
+    h = group_norm(x, groups, w[f"{p}.norm1.weight"], w[f"{p}.norm1.bias"], eps, silu=True)
+    h = conv2d(h, w[f"{p}.conv1.weight"], w[f"{p}.conv1.bias"], 1, 1)
+    proj = linear(silu_temb, w[f"{p}.time_emb_proj.weight"], w[f"{p}.time_emb_proj.bias"])
+    h = h + proj.reshape(h.shape[0], h.shape[1], 1, 1)
+    h = group_norm(h, groups, w[f"{p}.norm2.weight"], w[f"{p}.norm2.bias"], eps, silu=True)
+    h = conv2d(h, w[f"{p}.conv2.weight"], w[f"{p}.conv2.bias"], 1, 1)
+    if f"{p}.conv_shortcut.weight" in w:
+        x = conv2d(x, w[f"{p}.conv_shortcut.weight"], w[f"{p}.conv_shortcut.bias"], 1, 0)
+    return x + h
+
+
+def sdxl_transformer_block(x, context, w: dict, p: str, heads, eps=1e-5):
+    """UNetModel.TransformerBlock, UNetModel.cs:258-276, with
+    UNetLayers.DiffusersAttention (:14-26) and Geglu (:30-47). x [B, N, C],
+    context [B, Nc, Cw]."""
+    x = _f32(x)
+
+    def attend(h, src, a):
+        q = linear(h, w[f"{p}.{a}.to_q.weight"])
+        k = linear(src, w[f"{p}.{a}.to_k.weight"])
+        v = linear(src, w[f"{p}.{a}.to_v.weight"])
+        return linear(mha(q, k, v, heads), w[f"{p}.{a}.to_out.0.weight"], w[f"{p}.{a}.to_out.0.bias"])
+
+    h = layer_norm(x, w[f"{p}.norm1.weight"], w[f"{p}.norm1.bias"], eps)
+    x = x + attend(h, h, "attn1")
+    h = layer_norm(x, w[f"{p}.norm2.weight"], w[f"{p}.norm2.bias"], eps)
+    x = x + attend(h, _f32(context), "attn2")
+    h = layer_norm(x, w[f"{p}.norm3.weight"], w[f"{p}.norm3.bias"], eps)
+    proj = linear(h, w[f"{p}.ff.net.0.proj.weight"], w[f"{p}.ff.net.0.proj.bias"])
+    inner = proj.shape[-1] // 2
+    gated = proj[..., :inner] * gelu(np.ascontiguousarray(proj[..., inner:]))
+    return x + linear(gated, w[f"{p}.ff.net.2.weight"], w[f"{p}.ff.net.2.bias"])
+
+
+def sdxl_transformer2d(x, context, w: dict, p: str, heads, layers, groups=32, eps=1e-6, ln_eps=1e-5):
+    """UNetModel.Transformer2d, UNetModel.cs:279-301. x [B, C, H, W]."""
+    x = _f32(x)
+    B, C, H, W = x.shape
+    n = group_norm(x, groups, w[f"{p}.norm.weight"], w[f"{p}.norm.bias"], eps)
+    t = linear(n.reshape(B, C, H * W).transpose(0, 2, 1), w[f"{p}.proj_in.weight"], w[f"{p}.proj_in.bias"])
+    for j in range(layers):
+        t = sdxl_transformer_block(t, context, w, f"{p}.transformer_blocks.{j}", heads, ln_eps)
+    t = linear(t, w[f"{p}.proj_out.weight"], w[f"{p}.proj_out.bias"])
+    return t.transpose(0, 2, 1).reshape(B, C, H, W) + x
+
+
+def sdxl_unet(sample, time, add, context, w: dict, cfg):
+    """UNetModel.Build, UNetModel.cs:328-426, in fp32. sample [B, 4, h, w],
+    time [B, c0], add [B, add_width], context [B, tokens, Cw]; cfg carries
+    block_out, layers_per_block, transformer_layers, heads, groups, eps,
+    transformer_eps, layer_norm_eps."""
+    def mlp(x, prefix):
+        h = silu(linear(x, w[f"{prefix}.linear_1.weight"], w[f"{prefix}.linear_1.bias"]))
+        return linear(h, w[f"{prefix}.linear_2.weight"], w[f"{prefix}.linear_2.bias"])
+
+    def unit(x, prefix, index, level):
+        x = sdxl_resnet(x, st, w, f"{prefix}.resnets.{index}", cfg.groups, cfg.eps)
+        if cfg.transformer_layers[level]:
+            x = sdxl_transformer2d(x, context, w, f"{prefix}.attentions.{index}", cfg.heads[level],
+                                   cfg.transformer_layers[level], cfg.groups, cfg.transformer_eps, cfg.layer_norm_eps)
+        return x
+
+    st = silu(mlp(time, "time_embedding") + mlp(add, "add_embedding"))
+    skips = [conv2d(sample, w["conv_in.weight"], w["conv_in.bias"], 1, 1)]
+    levels = len(cfg.block_out)
+    for level in range(levels):
+        prefix = f"down_blocks.{level}"
+        for i in range(cfg.layers_per_block):
+            skips.append(unit(skips[-1], prefix, i, level))
+        if level != levels - 1:
+            skips.append(conv2d(skips[-1], w[f"{prefix}.downsamplers.0.conv.weight"],
+                                w[f"{prefix}.downsamplers.0.conv.bias"], 2, 1))
+    x = sdxl_resnet(skips[-1], st, w, "mid_block.resnets.0", cfg.groups, cfg.eps)
+    x = sdxl_transformer2d(x, context, w, "mid_block.attentions.0", cfg.heads[-1], cfg.transformer_layers[-1],
+                           cfg.groups, cfg.transformer_eps, cfg.layer_norm_eps)
+    x = sdxl_resnet(x, st, w, "mid_block.resnets.1", cfg.groups, cfg.eps)
+    for i in range(levels):
+        level = levels - 1 - i
+        prefix = f"up_blocks.{i}"
+        for j in range(cfg.layers_per_block + 1):
+            x = np.concatenate([x, skips.pop()], axis=1)
+            x = unit(x, prefix, j, level)
+        if i != levels - 1:
+            nxt = skips[-1].shape
+            up = upsample_nearest(x, 2)[:, :, :nxt[2], :nxt[3]]
+            x = conv2d(up, w[f"{prefix}.upsamplers.0.conv.weight"], w[f"{prefix}.upsamplers.0.conv.bias"], 1, 1)
+    x = group_norm(x, cfg.groups, w["conv_norm_out.weight"], w["conv_norm_out.bias"], cfg.eps, silu=True)
+    return conv2d(x, w["conv_out.weight"], w["conv_out.bias"], 1, 1)

@@ -501,6 +501,37 @@ API void orc_mmdit_rope_tables(int rows, int cols, int text_rows, float* cos_out
         }
 }
 
+/* ---- Anima inputs (Models/Anima) ------------------------------------------- */
+
+/* AnimaDit.RopeTables, AnimaDit.cs:149-188: per patch (i, j) of a rows x cols
+ * grid (row-major tokens), head_dim / 2 pairs: the first (head_dim - 2s) / 2
+ * temporal pairs still (a single frame), then s / 2 pairs turning with the
+ * row and s / 2 with the column, s = head_dim / 6 * 2, at frequencies
+ * 1 / theta^(2k / s) with theta = 10000 * 4^(s / (s - 2)) (the NTK factor),
+ * all in fp32. [tokens, head_dim / 2]. */
+API void orc_anima_rope_tables(int rows, int cols, int head_dim, float* cos_out, float* sin_out) {
+    int spatial = head_dim / 6 * 2, temporal = head_dim - 2 * spatial, pairs = head_dim / 2;
+    double ntk = pow(4.0, spatial / (double)(spatial - 2));
+    float theta = (float)(10000.0 * ntk);
+    float freq[64];
+    for (int k = 0; k < spatial / 2; k++) freq[k] = 1.0f / powf(theta, 2.0f * k / spatial);
+    for (int i = 0; i < rows; i++)
+        for (int j = 0; j < cols; j++) {
+            size_t off = (size_t)(i * cols + j) * pairs;
+            for (int d = 0; d < temporal / 2; d++) {
+                cos_out[off + d] = 1.0f;
+                sin_out[off + d] = 0.0f;
+            }
+            for (int k = 0; k < spatial / 2; k++) {
+                float ra = i * freq[k], ca = j * freq[k];
+                cos_out[off + temporal / 2 + k] = cosf(ra);
+                sin_out[off + temporal / 2 + k] = sinf(ra);
+                cos_out[off + temporal / 2 + spatial / 2 + k] = cosf(ca);
+                sin_out[off + temporal / 2 + spatial / 2 + k] = sinf(ca);
+            }
+        }
+}
+
 /* QwenImageConditioning.CausalTable, QwenImageConditioner.cs:69-80: row i
  * reads keys 0..min(i, real - 1). */
 API void orc_causal_table(int real, int rows, int32_t* out) {

@@ -1,0 +1,123 @@
+"""GPU parity of the convolution (Layers.Conv2d, Graph/Layers.cs:115-127 ->
+DmlOps.Convolution, Dml/DmlOps.cs:265-299) against the oracle's direct
+cross-correlation: the implicit-GEMM kernel at SDXL's shapes (3x3 pad 1,
+the stride-2 downsampler, the 1x1 shortcut with the resnet's residual add)
+scaled down in extent, ragged extents that leave partial pixel tiles, every
+tile variant pinned, and the direct kernel for what the implicit GEMM does
+not take (4 input channels, int8 filters). Tolerance: max|gpu - oracle| /
+max|oracle| <= 1e-2 at fp16, 2e-2 at bf16."""
+
+import numpy as np
+import pytest
+
+import naivediffusion_amd as nd
+import oracle
+from naivediffusion_amd import rng
+from naivediffusion_amd.layers import Layers
+from naivediffusion_amd.tensors import HostDataType as DT, HostTensor
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = {DT.Float16: 1e-2, DT.BFloat16: 2e-2}
+
+
+def normal(name, shape, std=1.0):
+    return rng.normal(rng.tensor_seed(11, name), shape, 0.0, std)
+
+
+def narrow(x, dtype):
+    """x rounded to dtype, as fp32 values (what the device holds)."""
+    return HostTensor.FromFloats(np.asarray(x, np.float32)).ConvertTo(dtype).ToFloats().reshape(np.shape(x))
+
+
+def run_conv(device, dtype, x, w, b, stride, pad, residual=None, int8=False):
+    model = nd.ModelBuilder(device, dtype, int8Weights=int8)
+    xin = model.Placeholder(list(x.shape), dtype)
+    rin = model.Placeholder(list(residual.shape), dtype) if residual is not None else None
+    y = Layers.Conv2d(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b), stride, pad, residual=rin)
+    model.Compile([y])
+    model.Compiled.SetProfiling(True)
+    inputs = [HostTensor.FromFloats(x).ConvertTo(dtype)]
+    if residual is not None:
+        inputs.append(HostTensor.FromFloats(residual).ConvertTo(dtype))
+    out = model.Run(*inputs)[0].ToFloats()
+    families = set(model.Compiled.Profile())
+    model.Dispose()
+    return out, families
+
+
+CASES = [
+    # (batch, Cin, H, W, Cout, k, stride, pad): SDXL's resnet conv at 320 and
+    # 640 channels, the downsampler, the 1x1 shortcut, a 1280-channel
+    # output that takes the 256-row tile, and extents that are not multiples
+    # of the pixel tile.
+    (1, 320, 24, 20, 320, 3, 1, 1),
+    (2, 64, 17, 15, 128, 3, 2, 1),
+    (1, 128, 16, 16, 64, 1, 1, 0),
+    (2, 640, 8, 8, 1280, 3, 1, 1),
+    (1, 192, 9, 31, 96, 3, 1, 1),
+]
+
+
+@pytest.mark.parametrize("B,Cin,H,W,Cout,k,stride,pad", CASES)
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16])
+def test_conv_implicit_gemm(device, B, Cin, H, W, Cout, k, stride, pad, dtype):
+    print(f"[gpu] conv {B}x{Cin}x{H}x{W} -> {Cout} k{k} s{stride} p{pad} {dtype.name}", flush=True)
+    x = narrow(normal("x", (B, Cin, H, W)), dtype)
+    w = narrow(normal("w", (Cout, Cin, k, k), 1.0 / np.sqrt(Cin * k * k)), dtype)
+    b = narrow(normal("b", (Cout,), 0.1), dtype)
+    out, families = run_conv(device, dtype, x, w, b, stride, pad)
+    ref = oracle.conv2d(x, w, b, stride, pad)
+    assert out.shape == ref.shape
+    assert any(f.startswith("conv_mfma_") for f in families), families
+    assert "nchw_to_nhwc" in families, families
+    err = rel_err(out, ref)
+    print(f"[gpu]   rel err {err:.2e} via {sorted(families)}", flush=True)
+    assert err <= TOL[dtype]
+
+
+def test_conv_residual_is_fused(device):
+    """The resnet's x + h rides the convolution's epilogue: conv(x) + r
+    rounded once at fp16, as Cast(h) + r."""
+    dtype = DT.Float16
+    x = narrow(normal("rx", (2, 128, 12, 10)), dtype)
+    w = narrow(normal("rw", (64, 128, 3, 3), 1.0 / np.sqrt(128 * 9)), dtype)
+    b = narrow(normal("rb", (64,), 0.1), dtype)
+    r = narrow(normal("rr", (2, 64, 12, 10)), dtype)
+    out, families = run_conv(device, dtype, x, w, b, 1, 1, residual=r)
+    assert rel_err(out, oracle.conv2d(x, w, b, 1, 1) + r) <= TOL[dtype]
+    assert any(f.startswith("conv_mfma_") for f in families), families
+
+
+@pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64"])
+def test_conv_every_tile(device, monkeypatch, tile):
+    print(f"[gpu] pinned conv tile {tile}", flush=True)
+    monkeypatch.setenv("NDX_CONV_TILE", tile)
+    dtype = DT.Float16
+    x = narrow(normal("tx", (2, 128, 13, 11)), dtype)
+    w = narrow(normal("tw", (300, 128, 3, 3), 1.0 / np.sqrt(128 * 9)), dtype)
+    b = narrow(normal("tb", (300,), 0.1), dtype)
+    out, families = run_conv(device, dtype, x, w, b, 1, 1)
+    want = {"256": "conv_mfma_256x256", "128": "conv_mfma_128x128", "64x128": "conv_mfma_64x128",
+            "64x64": "conv_mfma_64x64"}[tile]
+    assert want in families, families
+    assert rel_err(out, oracle.conv2d(x, w, b, 1, 1)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("case", ["conv_in", "int8"])
+def test_conv_direct_path(device, case):
+    """SDXL's conv_in (4 latent channels) and int8 filters stay on the direct kernel."""
+    dtype = DT.Float16
+    cin = 4 if case == "conv_in" else 64
+    x = narrow(normal("dx", (2, cin, 16, 12)), dtype)
+    w = narrow(normal("dw", (320 if case == "conv_in" else 128, cin, 3, 3), 1.0 / np.sqrt(cin * 9)), dtype)
+    b = narrow(normal("db", (w.shape[0],), 0.1), dtype)
+    out, families = run_conv(device, dtype, x, w, b, 1, 1, int8=case == "int8")
+    wq = w
+    if case == "int8":
+        rows = w.shape[0]
+        q, sc = oracle.quantize(w.reshape(rows, -1), rows)
+        wq = (q.astype(np.float32).reshape(rows, -1, 32) * oracle.f16_bits_to_f32(sc)[:, :, None]).reshape(w.shape)
+    assert not any(f.startswith("conv_mfma_") for f in families), families
+    assert rel_err(out, oracle.conv2d(x, wq, b, 1, 1)) <= TOL[dtype]

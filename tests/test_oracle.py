@@ -505,3 +505,116 @@ def test_mmdit_block_invariants():
     sp = np.concatenate([sin[:6][perm], sin[6:]])
     pi, pt = oracle.mmdit_block(xi[perm], xt, temb, img, txt, 2, np.ascontiguousarray(cp), np.ascontiguousarray(sp))
     assert np.max(np.abs(pi - yi[perm])) < 1e-5 and np.max(np.abs(pt - yt)) < 1e-5
+
+
+# ---- Anima (Models/Anima/AnimaDit.cs) ------------------------------------------------
+
+def test_anima_rotary_tables_leave_the_temporal_pairs_still():
+    # TransformerInputsTests.AnimasRotaryTablesLeaveTheTemporalPairsStill (:67-83).
+    c, s = oracle.anima_rope_tables(2, 2, 128)
+    assert c.shape == (4, 64)
+    assert np.all(c[:, :22] == 1) and np.all(s[:, :22] == 0)
+    assert abs(s[2, 22] - math.sin(1.0)) <= 1e-6, "row 1, column 0"
+    assert abs(s[1, 22 + 21] - math.sin(1.0)) <= 1e-6, "row 0, column 1"
+    assert s[1, 22] == 0, "row 0 does not turn with the row"
+
+
+def test_anima_rotary_frequencies_carry_the_ntk_factor():
+    # 21 pairs per spatial axis at 1 / theta^(2k/42), theta = 10000 * 4^(42/40).
+    c, s = oracle.anima_rope_tables(5, 7, 128)
+    theta = 10000.0 * 4.0 ** (42 / 40)
+    freq = 1.0 / theta ** (2.0 * np.arange(21) / 42)
+    i, j = 3, 5
+    tok = i * 7 + j
+    assert np.allclose(c[tok, 22:43], np.cos(i * freq), atol=2e-6)
+    assert np.allclose(s[tok, 43:64], np.sin(j * freq), atol=2e-6)
+    # A head of 64 features: 20 per spatial axis, 24 temporal.
+    c64, s64 = oracle.anima_rope_tables(2, 2, 64)
+    assert c64.shape == (4, 32) and np.all(c64[:, :12] == 1) and abs(s64[2, 12] - math.sin(1.0)) <= 1e-6
+
+
+def test_anima_patch_layouts_against_numpy_transposes():
+    C, H, W = 16, 6, 8
+    lat = r(40, C, H, W)
+    # Patchify: feature c*4 + m*2 + n (AnimaDit.cs:193-219).
+    exp = lat.reshape(C, H // 2, 2, W // 2, 2).transpose(1, 3, 0, 2, 4).reshape(-1, C * 4)
+    assert np.array_equal(oracle.anima_patchify(lat), exp)
+    # Unpatchify: feature (p1*2 + p2)*16 + c (AnimaDit.cs:223-247).
+    tok = r(41, (H // 2) * (W // 2), C * 4)
+    exp = tok.reshape(H // 2, W // 2, 2, 2, C).transpose(4, 0, 2, 1, 3).reshape(C, H, W)
+    assert np.array_equal(oracle.anima_unpatchify(tok, C, H, W), exp)
+
+
+def _tiny_anima(seed, D=64, heads=2, F=128, R=16, Cw=32, n=6, nc=5):
+    g = np.random.default_rng(seed)
+
+    def w(*shape, s=0.2):
+        return (g.standard_normal(shape) * s).astype(np.float32)
+
+    p = "blocks.0"
+    ws = {}
+    for part in ("self_attn", "cross_attn", "mlp"):
+        ws[f"{p}.adaln_modulation_{part}.1.weight"] = w(R, D)
+        ws[f"{p}.adaln_modulation_{part}.2.weight"] = w(3 * D, R)
+    for a, src in (("self_attn", D), ("cross_attn", Cw)):
+        ws[f"{p}.{a}.q_proj.weight"] = w(D, D)
+        ws[f"{p}.{a}.k_proj.weight"] = w(D, src)
+        ws[f"{p}.{a}.v_proj.weight"] = w(D, src)
+        ws[f"{p}.{a}.output_proj.weight"] = w(D, D)
+        ws[f"{p}.{a}.q_norm.weight"] = 1 + w(D // heads, s=0.1)
+        ws[f"{p}.{a}.k_norm.weight"] = 1 + w(D // heads, s=0.1)
+    ws[f"{p}.mlp.layer1.weight"] = w(F, D)
+    ws[f"{p}.mlp.layer2.weight"] = w(D, F)
+    x, temb, lora, ctx = w(n, D, s=1), w(D, s=1), w(3 * D, s=0.5), w(nc, Cw, s=1)
+    cos, sin = oracle.anima_rope_tables(2, 3, D // heads)
+    return ws, x, temb, lora, ctx, cos, sin
+
+
+def test_anima_block_invariants():
+    D = 64
+    ws, x, temb, lora, ctx, cos, sin = _tiny_anima(1)
+    # Zero modulation: every gate is 0 and the block is the identity.
+    z = {k: (np.zeros_like(v) if ".2.weight" in k and "adaln" in k else v) for k, v in ws.items()}
+    y = oracle.anima_block(x, temb, np.zeros_like(lora), ctx, z, 0, 2, cos, sin)
+    assert np.array_equal(y, x)
+    # The shared term alone: with W2 = 0 the modulation rows are the lora's.
+    parts = oracle.anima_modulation(temb, lora, ws["blocks.0.adaln_modulation_mlp.1.weight"],
+                                    np.zeros((3 * D, 16), np.float32), 3, D)
+    assert all(np.array_equal(parts[i], lora[i * D:(i + 1) * D]) for i in range(3))
+    two = oracle.anima_modulation(temb, lora, ws["blocks.0.adaln_modulation_mlp.1.weight"],
+                                  np.zeros((2 * D, 16), np.float32), 2, D)
+    assert np.array_equal(two[1], lora[D:2 * D])
+    # Cross-attention reads the context as keys: permuting its rows changes nothing.
+    y = oracle.anima_block(x, temb, lora, ctx, ws, 0, 2, cos, sin)
+    yp = oracle.anima_block(x, temb, lora, ctx[[3, 1, 4, 0, 2]], ws, 0, 2, cos, sin)
+    assert np.max(np.abs(y - yp)) < 1e-5
+    # Self-attention is equivariant: permuting the tokens with their rotary
+    # rows permutes the result.
+    perm = np.array([4, 0, 5, 2, 1, 3])
+    yq = oracle.anima_block(x[perm], temb, lora, ctx, ws, 0, 2, np.ascontiguousarray(cos[perm]),
+                            np.ascontiguousarray(sin[perm]))
+    assert np.max(np.abs(yq - y[perm])) < 1e-5
+
+
+def test_anima_mlp_branch_is_exact_gelu():
+    """Only the MLP's gate open (1) and shift/scale 0: x + W2 GELU(W1 LN(x)),
+    checked in float64 with scipy's erf, which tells the exact GELU from the
+    tanh form."""
+    from scipy.special import erf
+    D = 64
+    ws, x, temb, lora, ctx, cos, sin = _tiny_anima(2)
+    for part in ("self_attn", "cross_attn", "mlp"):
+        ws[f"blocks.0.adaln_modulation_{part}.2.weight"][:] = 0
+    lora = np.zeros(3 * D, np.float32)
+    # The parts share the lora: a gate of 1 for all three, then close the
+    # attention branches by zeroing their output projections.
+    lora[2 * D:3 * D] = 1
+    ws["blocks.0.self_attn.output_proj.weight"][:] = 0
+    ws["blocks.0.cross_attn.output_proj.weight"][:] = 0
+    y = oracle.anima_block(x, temb, lora, ctx, ws, 0, 2, cos, sin)
+    xd = x.astype(np.float64)
+    ln = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + 1e-6)
+    h = ln @ ws["blocks.0.mlp.layer1.weight"].astype(np.float64).T
+    f = 0.5 * h * (1 + erf(h / np.sqrt(2)))
+    exp = xd + f @ ws["blocks.0.mlp.layer2.weight"].astype(np.float64).T
+    assert np.max(np.abs(y - exp)) < 2e-5 * np.max(np.abs(exp - xd))
