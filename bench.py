@@ -8,7 +8,8 @@ flops per launch over its HIP-event-timed average launch), and the CPU
 baseline (the oracle's restatement of the reference's C# CPU layer path,
 timed on this host over one block of the same step and scaled to 60 blocks).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--compute bf16|f32|f16] [--no-cpu-baseline]
+    python bench.py --workload anima|sdxl   # the Anima DiT / SDXL UNet steps (their own lines)
     python bench.py --calibrate-copy    # a plain 1 GiB device copy, for scaling HBM counters
 
 The roofline's `traffic` (HBM bytes per launch of the dominant kernel) is
@@ -31,6 +32,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (and fp16)
+FP32_PEAK_TFLOPS = 157.3         # MI355X fp32 matrix
 HBM_PEAK_GBS = 8000.0
 
 
@@ -61,9 +63,10 @@ def calibrate_copy(reps=5):
                       "launches": reps}), flush=True)
 
 
-def read_traffic(kernel):
-    """HBM bytes per launch of `kernel` from its committed counter summary."""
-    for path in sorted((ROOT / "profiles").glob(f"{kernel}_*traffic*.md")):
+def read_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` in `workload` from its committed
+    counter summary (profiles/<kernel>_<workload>_..._traffic.md)."""
+    for path in sorted((ROOT / "profiles").glob(f"{kernel}_{workload}_*traffic*.md")):
         for line in path.read_text().splitlines():
             if line.strip().startswith("bytes_per_launch:"):
                 return float(line.split(":", 1)[1].split()[0]), path.name
@@ -120,13 +123,178 @@ def cpu_baseline(device, cfg, seed, ni, nt):
     }
 
 
+def measure(dev, compiled, inputs, out, steps, warmup):
+    """W untimed steps, then K timed steps with every kernel bracketed by
+    HIP events on the device's stream (the stream all kernels run on)."""
+    for _ in range(warmup):
+        compiled.DispatchInto(inputs, out)
+    dev.Synchronize()
+    log(f"warmup done ({warmup} steps)")
+    compiled.SetProfiling(True)
+    dev.Synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        compiled.DispatchInto(inputs, out)
+    dev.Synchronize()
+    elapsed = time.perf_counter() - t0
+    prof = compiled.Profile()
+    compiled.SetProfiling(False)
+    log(f"{steps} steps in {elapsed:.3f} s: {elapsed / steps * 1e3:.1f} ms/step")
+    for name, e in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        tf = e["flops"] / (e["ms"] * 1e-3) / 1e12 if e["ms"] else 0.0
+        gbs = e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] else 0.0
+        log(f"  {name:28s} {e['launches'] // steps:5d}/step {e['ms'] / steps:9.2f} ms/step "
+            f"{tf:8.1f} TFLOP/s {gbs:8.1f} GB/s")
+    return elapsed / steps, prof
+
+
+def roofline(prof, steps, peak, workload):
+    """The dominant MFMA kernel family (GEMM, convolution or attention) by
+    time: algorithmic flops per launch over its event-timed average launch."""
+    mfma = {k: v for k, v in prof.items()
+            if (k.startswith("gemm_") and "generic" not in k) or k.startswith("conv_mfma") or k.startswith("attention")}
+    name, dom = max(mfma.items(), key=lambda kv: kv[1]["ms"])
+    per_launch = dom["flops"] / dom["launches"]
+    avg_ms = dom["ms"] / dom["launches"]
+    achieved = per_launch / (avg_ms * 1e-3) / 1e12
+    traffic, src = read_traffic(name, workload)
+    return {
+        "bound": "mfma", "kernel": name, "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+        "frac": achieved / peak, "traffic": traffic, "traffic_unit": "bytes/launch", "traffic_source": src,
+        "algorithmic_flop_per_launch": per_launch, "launches_per_step": dom["launches"] // steps,
+        "avg_launch_ms": avg_ms,
+    }
+
+
+def setup_mmdit(args, dev, seed, DT):
+    from naivediffusion_amd import mmdit, rng
+    from naivediffusion_amd.tensors import HostTensor
+
+    cfg = mmdit.MmditConfig(blocks=args.blocks or 60)
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    lat_h, lat_w, nt = 128, 168, 256
+    ni = (lat_h // cfg.patch) * (lat_w // cfg.patch)
+    t0 = time.perf_counter()
+    weights = mmdit.device_weights(dev, cfg, seed)
+    log(f"synthetic weights on the device in {time.perf_counter() - t0:.1f} s")
+    model = mmdit.build_step_model(dev, cfg, weights, 1, nt, lat_h, lat_w, compute, args.int8)
+    n = ni + nt
+    cos, sin = mmdit.rope_tables(lat_h // cfg.patch, lat_w // cfg.patch, nt)
+    inputs = [
+        dev.Normal(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w], rng.tensor_seed(seed, "latent")),
+        dev.Normal(DT.Float32, [1, 1, nt, cfg.text_dim], rng.tensor_seed(seed, "text")),
+        dev.Upload(HostTensor.FromFloats(mmdit.time_embedding(0.5, cfg.time_dim).reshape(1, 1, 1, cfg.time_dim))),
+        dev.Upload(HostTensor.FromFloats(cos.reshape(1, n, 1, 64))),
+        dev.Upload(HostTensor.FromFloats(sin.reshape(1, n, 1, 64))),
+    ]
+    out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w])]
+    wdesc = "int8 block-32 weights" if args.int8 else f"{args.compute} weights"
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="Qwen-Image DiT s/step @1024x1344 (bf16/int8 wts), 1 MI355X; % MFMA peak",
+        config={"workload": (f"Qwen-Image-shaped MMDiT denoiser step, {cfg.blocks} dual-stream blocks, 1024x1344 "
+                             f"(latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), hidden 3072, "
+                             f"24x128 heads, MLP 12288, batch 1, {args.compute} compute, {wdesc}"),
+                "blocks": cfg.blocks, "image_tokens": ni, "text_tokens": nt,
+                "weights": "int8" if args.int8 else args.compute},
+        data="synthetic (seeded N(0,1) latent and text, N(0,0.02) bf16 weights made on the GPU)",
+        cpu=lambda: cpu_baseline(dev, cfg, seed, ni, nt),
+    )
+
+
+def setup_anima(args, dev, seed, DT):
+    from naivediffusion_amd import anima, rng
+    from naivediffusion_amd.layers import Transformer
+    from naivediffusion_amd.tensors import HostTensor
+
+    cfg = anima.AnimaConfig(blocks=args.blocks or 28)
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    store = compute if compute != DT.Float32 else DT.Float16
+    lat, n_ctx = 128, 512
+    n = (lat // 2) ** 2
+    weights = anima.device_weights(dev, cfg, seed, store)
+    model = anima.build_step_model(dev, cfg, weights, lat, lat, n_ctx, compute, args.int8)
+    cos, sin = anima.rope_tables(lat // 2, lat // 2, cfg.head_dim)
+    half = cfg.head_dim // 2
+    inputs = [
+        dev.Normal(DT.Float32, [1, cfg.latent_channels, lat, lat], rng.tensor_seed(seed, "latent")),
+        dev.Upload(HostTensor.FromFloats(Transformer.Sinusoid(0.5, cfg.width).reshape(1, 1, 1, cfg.width))),
+        dev.Normal(DT.Float32, [1, 1, n_ctx, cfg.context_width], rng.tensor_seed(seed, "context")),
+        dev.Upload(HostTensor.FromFloats(cos.reshape(1, n, 1, half))),
+        dev.Upload(HostTensor.FromFloats(sin.reshape(1, n, 1, half))),
+    ]
+    out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat, lat])]
+
+    def cpu():
+        import oracle
+        names = list(anima.block_weight_shapes(cfg, 0))
+        dw = anima.device_weights(dev, cfg, seed, DT.BFloat16, names)
+        w = {k: t.Download().ToFloats() for k, t in dw.items()}
+        for t in dw.values():
+            t.Dispose()
+        x = dev.Normal(DT.Float32, [n, cfg.width], rng.tensor_seed(seed, "cpu.x")).Download().ToFloats()
+        ctx = inputs[2].Download().ToFloats().reshape(n_ctx, cfg.context_width)
+        tmb = Transformer.Sinusoid(0.5, cfg.width)
+        lora = np.zeros(3 * cfg.width, np.float32)
+        threads = len(os.sched_getaffinity(0))
+        t0 = time.perf_counter()
+        oracle.anima_block(x, tmb, lora, ctx, w, 0, cfg.heads, cos, sin)
+        dt = time.perf_counter() - t0
+        return {"value": dt * cfg.blocks, "unit": "s/step", "cores": threads, "kind": "port",
+                "sample": (f"one Anima block ({n} tokens, context {n_ctx}, hidden {cfg.width}, fp32) on the oracle "
+                           f"in {dt:.2f} s, x{cfg.blocks} blocks (extrapolated)")}
+
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="Anima DiT s/step @1024x1024, 1 MI355X; % MFMA peak",
+        config={"workload": (f"Anima-shaped 2B DiT denoiser step, {cfg.blocks} blocks, 1024x1024 (latent 16x{lat}x{lat}, "
+                             f"2x2 patch: {n} tokens), hidden 2048, 16x128 heads, MLP 8192, cross-attention to "
+                             f"{n_ctx}x1024 context, batch 1, {args.compute} compute"),
+                "blocks": cfg.blocks, "tokens": n, "context_rows": n_ctx},
+        data="synthetic (seeded N(0,1) latent and context, N(0,0.02) weights made on the GPU)",
+        cpu=cpu,
+    )
+
+
+def setup_sdxl(args, dev, seed, DT):
+    from naivediffusion_amd import rng, sdxl
+    from naivediffusion_amd.tensors import HostTensor
+
+    cfg = sdxl.SdxlConfig()
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    B, lat, tokens = 2, 128, 77
+    weights = sdxl.device_weights(dev, cfg, seed, compute)
+    model = sdxl.build_unet(dev, cfg, weights, B, lat, lat, tokens, compute, args.int8)
+    t = np.tile(sdxl.timestep_embedding([500.0], cfg.block_out[0]), (B, 1)).reshape(B, 1, 1, -1)
+    add = np.stack([sdxl.add_conditioning(np.zeros(cfg.pooled_width, np.float32), add_time_dim=cfg.add_time_dim)] * B)
+    inputs = [
+        dev.Normal(compute, [B, cfg.in_channels, lat, lat], rng.tensor_seed(seed, "latent")),
+        dev.Upload(HostTensor.FromFloats(np.ascontiguousarray(t)).ConvertTo(compute)),
+        dev.Upload(HostTensor.FromFloats(add.reshape(B, 1, 1, -1)).ConvertTo(compute)),
+        dev.Normal(compute, [B, 1, tokens, cfg.context_width], rng.tensor_seed(seed, "context")),
+    ]
+    out = [dev.Empty(compute, [B, cfg.in_channels, lat, lat])]
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="SDXL UNet s/step @1024x1024 CFG batch 2, 1 MI355X; % MFMA peak",
+        config={"workload": (f"SDXL UNet step, 1024x1024 (latent 4x{lat}x{lat}), CFG batch {B}, context {tokens}x2048, "
+                             f"{args.compute} compute"), "batch": B},
+        data="synthetic (seeded N(0,1) latent and context, N(0,0.02) weights made on the GPU)",
+        cpu=None,
+    )
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--int8", action="store_true", help="int8 block-quantised weights (bf16 compute)")
-    ap.add_argument("--blocks", type=int, default=60)
+    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl"], default="mmdit",
+                    help="mmdit (the headline), or the Anima DiT / SDXL UNet steps")
+    ap.add_argument("--compute", choices=["bf16", "f32", "f16"], default=None,
+                    help="compute type (default bf16; fp16 for sdxl)")
+    ap.add_argument("--int8", action="store_true", help="int8 block-quantised weights")
+    ap.add_argument("--blocks", type=int, default=None, help="block count (default: the model's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")
     args = ap.parse_args()
@@ -140,81 +308,43 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
+    if args.compute is None:
+        args.compute = "f16" if args.workload == "sdxl" else "bf16"
 
     import naivediffusion_amd as nd
-    from naivediffusion_amd import mmdit, rng
-    from naivediffusion_amd.tensors import HostDataType as DT, HostTensor
+    from naivediffusion_amd.tensors import HostDataType as DT
 
-    cfg = mmdit.MmditConfig(blocks=args.blocks)
-    lat_h, lat_w, nt = 128, 168, 256
-    ni = (lat_h // cfg.patch) * (lat_w // cfg.patch)
     seed = 20261201
     dev = nd.Device()
     log(f"device {dev.AdapterName}")
-
     t0 = time.perf_counter()
-    weights = mmdit.device_weights(dev, cfg, seed)
-    log(f"synthetic weights on the device in {time.perf_counter() - t0:.1f} s")
-    t0 = time.perf_counter()
-    model = mmdit.build_step_model(dev, cfg, weights, 1, nt, lat_h, lat_w, DT.BFloat16, args.int8)
-    compiled = model.Compiled
+    setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl}[args.workload](args, dev, seed, DT)
+    compiled = setup["model"].Compiled
     log(f"graph built and compiled in {time.perf_counter() - t0:.1f} s: {compiled.KernelCount} kernels/step, "
         f"{compiled.PersistentSize / 1e9:.1f} GB weights, {compiled.TemporarySize / 1e9:.2f} GB scratch")
 
-    n = ni + nt
-    cos, sin = mmdit.rope_tables(lat_h // cfg.patch, lat_w // cfg.patch, nt)
-    inputs = [
-        dev.Normal(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w], rng.tensor_seed(seed, "latent")),
-        dev.Normal(DT.Float32, [1, 1, nt, cfg.text_dim], rng.tensor_seed(seed, "text")),
-        dev.Upload(HostTensor.FromFloats(mmdit.time_embedding(0.5, cfg.time_dim).reshape(1, 1, 1, cfg.time_dim))),
-        dev.Upload(HostTensor.FromFloats(cos.reshape(1, n, 1, 64))),
-        dev.Upload(HostTensor.FromFloats(sin.reshape(1, n, 1, 64))),
-    ]
-    out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w])]
-
-    for i in range(args.warmup):
-        compiled.DispatchInto(inputs, out)
-    dev.Synchronize()
-    log(f"warmup done ({args.warmup} steps)")
-
-    # Timed region: every kernel bracketed by HIP events on the device's
-    # stream (the stream all kernels are launched on).
-    compiled.SetProfiling(True)
-    dev.Synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        compiled.DispatchInto(inputs, out)
-    dev.Synchronize()
-    elapsed = time.perf_counter() - t0
-    prof = compiled.Profile()
-    compiled.SetProfiling(False)
-    s_per_step = elapsed / args.steps
-    log(f"{args.steps} steps in {elapsed:.3f} s: {s_per_step * 1e3:.1f} ms/step")
-
+    s_per_step, prof = measure(dev, compiled, setup["inputs"], setup["out"], args.steps, args.warmup)
+    peak = FP32_PEAK_TFLOPS if args.compute == "f32" else MFMA_BF16_PEAK_TFLOPS
     total_flops = sum(e["flops"] for e in prof.values()) / args.steps
     kernel_ms = sum(e["ms"] for e in prof.values()) / args.steps
-    for name, e in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
-        tf = e["flops"] / (e["ms"] * 1e-3) / 1e12 if e["ms"] else 0.0
-        gbs = e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] else 0.0
-        log(f"  {name:28s} {e['launches'] // args.steps:5d}/step {e['ms'] / args.steps:9.2f} ms/step "
-            f"{tf:8.1f} TFLOP/s {gbs:8.1f} GB/s")
-    gemm = {k: v for k, v in prof.items() if k.startswith("gemm_") and "generic" not in k}
-    dom_name, dom = max(gemm.items(), key=lambda kv: kv[1]["ms"])
-    per_launch_flops = dom["flops"] / dom["launches"]
-    avg_ms = dom["ms"] / dom["launches"]
-    achieved = per_launch_flops / (avg_ms * 1e-3) / 1e12
-    traffic, traffic_src = read_traffic(dom_name)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and setup["cpu"] is not None:
         try:
-            cpu = cpu_baseline(dev, cfg, seed, ni, nt)
+            cpu = setup["cpu"]()
             log(f"cpu baseline {cpu['value']:.1f} s/step ({cpu['cores']} threads)")
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline failed: {e!r}")
 
+    config = dict(setup["config"])
+    config.update({
+        "algorithmic_tflop_per_step": total_flops / 1e12,
+        "achieved_tflops_step": total_flops / s_per_step / 1e12,
+        "step_frac_of_mfma_peak": total_flops / s_per_step / 1e12 / peak,
+        "kernel_ms_per_step": kernel_ms,
+    })
     result = {
-        "metric": "Qwen-Image DiT s/step @1024x1344 (bf16/int8 wts), 1 MI355X; % MFMA peak",
+        "metric": setup["metric"],
         "value": s_per_step,
         "unit": "s/step",
         "n_gpus": 1,
@@ -224,36 +354,10 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) latent and text, N(0,0.02) bf16 weights made on the GPU)",
-        "config": {
-            "workload": (f"Qwen-Image-shaped MMDiT denoiser step, {cfg.blocks} dual-stream blocks, 1024x1344 "
-                         f"(latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), hidden 3072, "
-                         f"24x128 heads, MLP 12288, batch 1, "
-                         + ("int8 block-32 weights" if args.int8 else "bf16 weights")),
-            "blocks": cfg.blocks,
-            "image_tokens": ni,
-            "text_tokens": nt,
-            "weights": "int8" if args.int8 else "bf16",
-            "algorithmic_tflop_per_step": total_flops / 1e12,
-            "achieved_tflops_step": total_flops / s_per_step / 1e12,
-            "step_frac_of_mfma_peak": total_flops / s_per_step / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-            "kernel_ms_per_step": kernel_ms,
-        },
-        "roofline": {
-            "bound": "mfma",
-            "kernel": dom_name,
-            "achieved": achieved,
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": traffic,
-            "traffic_unit": "bytes/launch",
-            "traffic_source": traffic_src,
-            "algorithmic_flop_per_launch": per_launch_flops,
-            "launches_per_step": dom["launches"] // args.steps,
-            "avg_launch_ms": avg_ms,
-        },
+        "dtype": args.compute,
+        "data": setup["data"],
+        "config": config,
+        "roofline": roofline(prof, args.steps, peak, args.workload),
         "kernels": {k: {"ms_per_step": v["ms"] / args.steps, "launches_per_step": v["launches"] // args.steps,
                         "tflops": (v["flops"] / (v["ms"] * 1e-3) / 1e12) if v["ms"] else 0.0,
                         "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] else 0.0}

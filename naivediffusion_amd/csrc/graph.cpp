@@ -66,6 +66,8 @@ struct GNode {
   float f0 = 0.f, f1 = 0.f;
   // attention segments (compile-time rewrite): per q/k/v up to two values
   int seg[3][2] = {{-1, -1}, {-1, -1}, {-1, -1}};
+  // scratch in the arena, live only while this node runs
+  int64_t scratch_bytes = 0, scratch_off = -1;
   // profiling
   std::string family;
   double flops = 0, bytes = 0;
@@ -1251,7 +1253,14 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
           if (n.in[j] >= 0 && c.values[n.in[j]].v.size[3] > 1 && c.values[n.in[j]].v.stride[3] != 1)
             n.in[j] = c.pack(n.in[j], sched);
         break;
-      case OP_GROUPNORM:
+      case OP_GROUPNORM: {
+        for (auto& id : n.in)
+          if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
+        const View4& xv = c.values[n.in[0]].v;
+        const int64_t count = xv.size[1] / n.i0 * xv.size[2] * xv.size[3];
+        n.scratch_bytes = int64_t(xv.size[0]) * n.i0 * group_norm_splits(count) * 3 * sizeof(float);
+        break;
+      }
       case OP_PATCH:
         for (auto& id : n.in)
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
@@ -1333,20 +1342,27 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     };
     std::vector<Live> live;
     int64_t top = 0;
-    for (int i = 0; i < (int)m->nodes.size(); i++) {
-      int id = m->nodes[i].out;
-      if (m->out_slot[id] >= 0) continue;
-      live.erase(std::remove_if(live.begin(), live.end(), [&](const Live& l) { return l.last < i; }), live.end());
-      int64_t size = (int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype) + 255) & ~int64_t(255);
+    // First fit of [size] bytes among the live ranges; returns the offset.
+    auto place = [&](int64_t bytes, int until) {
+      int64_t size = (bytes + 255) & ~int64_t(255);
       std::sort(live.begin(), live.end(), [](const Live& a, const Live& b) { return a.off < b.off; });
       int64_t off = 0;
       for (const Live& l : live) {
         if (off + size <= l.off) break;
         off = std::max(off, l.off + l.size);
       }
-      m->arena_off[id] = off;
-      live.push_back({off, size, std::max(last[id], i)});
+      live.push_back({off, size, until});
       top = std::max(top, off + size);
+      return off;
+    };
+    for (int i = 0; i < (int)m->nodes.size(); i++) {
+      GNode& node = m->nodes[i];
+      int id = node.out;
+      live.erase(std::remove_if(live.begin(), live.end(), [&](const Live& l) { return l.last < i; }), live.end());
+      if (m->out_slot[id] < 0)
+        m->arena_off[id] =
+            place(int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype), std::max(last[id], i));
+      if (node.scratch_bytes > 0) node.scratch_off = place(node.scratch_bytes, i);
     }
     m->arena_bytes = (size_t)top;
     if (top > 0) {
@@ -1643,6 +1659,8 @@ struct Runner {
           a.bias = ptr(n.in[2]);
           a.w_dtype = val(n.in[2]).dtype;
         }
+        a.partial = (float*)((char*)m->arena + n.scratch_off);
+        a.splits = group_norm_splits(int64_t(a.C / a.groups) * a.HW);
         launch_group_norm(a, s);
         break;
       }

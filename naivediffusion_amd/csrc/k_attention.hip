@@ -14,8 +14,11 @@
 // keys are double buffered in LDS (V transposed on its way in), swizzled by
 // 16- and 8-byte granules.
 //
+// flash_attn_f32_kernel (fp32, d = 64 or 128): the same scheme on fp32
+// MFMA, described at the kernel.
+//
 // attn_generic_kernel: any float type and head size, fp32 arithmetic with
-// expf; the fp32-compute path and the reference for odd shapes.
+// expf; the path for odd shapes.
 
 #include <cstdlib>
 
@@ -283,6 +286,168 @@ __global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnAr
   }
 }
 
+// ---- fp32 ---------------------------------------------------------------------
+//
+// flash_attn_f32_kernel: the same transposed flash form on
+// v_mfma_f32_32x32x2_f32 (two K steps per instruction, one per lane half).
+// In the score product lane half h covers head features [h d/2, (h+1) d/2),
+// so each lane streams one contiguous half-row of K from LDS; in the output
+// product step s of a 32-key tile takes, in lane half h, the key of score
+// register s (row 8 (s / 4) + 4 h + s % 4 of S^T), so P^T again comes straight
+// from the score registers. K and V tiles of 64 keys sit in LDS row-major,
+// rows padded by 16 bytes; the next tile is prefetched into registers while
+// the current one is consumed.
+
+template <int D, int MASK>
+__global__ __launch_bounds__(256) void flash_attn_f32_kernel(AttnArgs a, int grid) {
+  constexpr int BQ = 128, BKEY = 64, LD = D + 4, DH = D / 2, DT = D / 32;
+  constexpr int F4 = BKEY * D / 4 / 256;  // float4 loads per thread per tile
+  __shared__ __attribute__((aligned(16))) float Ks[BKEY * LD];
+  __shared__ __attribute__((aligned(16))) float Vs[BKEY * LD];
+
+  int qb, head, b;
+  if (!attn_tile(blockIdx.x, grid, (a.T + BQ - 1) / BQ, a.H, a.B, qb, head, b)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lq = lane & 31, lh = lane >> 5;
+  const int64_t col0 = int64_t(head) * D;
+  const int qi = qb * BQ + wave * 32 + lq;
+  const int qm = min(qi, a.T - 1);
+
+  float qf[DH];
+  {
+    const float* qrow = seg_row<float>(a.q, b, qm) + col0 + lh * DH;
+#pragma unroll
+    for (int t = 0; t < DH; t += 4) *(float4*)&qf[t] = *(const float4*)(qrow + t);
+  }
+
+  float4 rk[F4], rv[F4];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < F4; i++) {
+      const int id = tid + i * 256;
+      const int key = id / (D / 4), c4 = id % (D / 4);
+      const int gk = kb * BKEY + key;
+      rk[i] = *(const float4*)(seg_row<float>(a.k, b, min(gk, a.S - 1)) + col0 + c4 * 4);
+      // Tail rows of V are zero: a zero probability times a stale value
+      // could still be NaN.
+      rv[i] = gk < a.S ? *(const float4*)(seg_row<float>(a.v, b, gk) + col0 + c4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store_kv = [&]() {
+#pragma unroll
+    for (int i = 0; i < F4; i++) {
+      const int id = tid + i * 256;
+      const int key = id / (D / 4), c4 = id % (D / 4);
+      *(float4*)&Ks[key * LD + c4 * 4] = rk[i];
+      *(float4*)&Vs[key * LD + c4 * 4] = rv[i];
+    }
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int j = 0; j < DT; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[j][r] = 0.f;
+  float m_run = -INFINITY, l_part = 0.f;
+  const float sl = a.scale * kLog2e;
+  const float mask_add = -10000.0f * kLog2e;
+  const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
+
+  const int KB = (a.S + BKEY - 1) / BKEY;
+  load_kv(0);
+  for (int kb = 0; kb < KB; kb++) {
+    __syncthreads();  // the previous tile is consumed
+    store_kv();
+    __syncthreads();
+    if (kb + 1 < KB) load_kv(kb + 1);
+
+    f32x16 sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
+    const float* k0 = &Ks[lq * LD + lh * DH];
+    const float* k1 = &Ks[(32 + lq) * LD + lh * DH];
+#pragma unroll
+    for (int t = 0; t < DH; t += 4) {
+      const float4 a0 = *(const float4*)(k0 + t);
+      const float4 a1 = *(const float4*)(k1 + t);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, qf[t], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, qf[t], sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, qf[t + 1], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, qf[t + 1], sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, qf[t + 2], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, qf[t + 2], sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, qf[t + 3], sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, qf[t + 3], sacc[1], 0, 0, 0);
+    }
+
+    const bool tail = (kb + 1) * BKEY > a.S;
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float x = sacc[kt][r] * sl;
+        const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (MASK == NDX_MASK_KEY_LENGTH) {
+          if (key >= key_len) x += mask_add;
+        } else if (MASK == NDX_MASK_BOOLEAN) {
+          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
+                             int64_t(min(key, a.S - 1)) * a.mask_stride[3];
+          if (a.mask[mi] == 0) x += mask_add;
+        }
+        if (tail && key >= a.S) x = -INFINITY;
+        sacc[kt][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+      const float alpha = exp2f(m_run - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int j = 0; j < DT; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+    }
+    m_run = m_new;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float p = exp2f(sacc[kt][r] - m_new);
+        sacc[kt][r] = p;
+        l_part += p;
+      }
+
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const int key = kt * 32 + 8 * (s >> 2) + 4 * lh + (s & 3);
+        const float* vrow = &Vs[key * LD + lq];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[dt * 32], sacc[kt][s], o[dt], 0, 0, 0);
+      }
+  }
+
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < a.T) {
+    float* orow = (float*)out_row(a, b, qi, sizeof(float)) + col0;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = dt * 32 + 8 * g + 4 * lh;
+        *(float4*)(orow + d) = make_float4(o[dt][g * 4] * inv, o[dt][g * 4 + 1] * inv, o[dt][g * 4 + 2] * inv,
+                                           o[dt][g * 4 + 3] * inv);
+      }
+  }
+}
+
 // ---- generic ----------------------------------------------------------------
 
 // 16 queries of one (batch, head) per workgroup, 4 per wave; 64-key tiles
@@ -420,6 +585,25 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
     }
 #undef NDX_FA_MASKS
 #undef NDX_FA
+    return;
+  }
+  const bool mfma32 = a.dtype == NDX_F32 && a.d == a.dv && (a.d == 128 || a.d == 64) && rows_aligned(a.q, 4) &&
+                      rows_aligned(a.k, 4) && rows_aligned(a.v, 4) && (uintptr_t)a.out[0] % 16 == 0 &&
+                      (uintptr_t)a.out[1] % 16 == 0 && (a.out_ld[0] * 4) % 16 == 0 && (a.out_ld[1] * 4) % 16 == 0;
+  if (mfma32) {
+    const int qblocks = (a.T + 127) / 128;
+    const int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
+#define NDX_FA32(DIM, MK) hipLaunchKernelGGL((flash_attn_f32_kernel<DIM, MK>), dim3(grid), dim3(256), 0, s, a, grid)
+#define NDX_FA32_MASKS(DIM)                                                \
+  do {                                                                     \
+    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA32(DIM, 1);              \
+    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA32(DIM, 2);            \
+    else NDX_FA32(DIM, 0);                                                 \
+  } while (0)
+    if (a.d == 128) NDX_FA32_MASKS(128);
+    else NDX_FA32_MASKS(64);
+#undef NDX_FA32_MASKS
+#undef NDX_FA32
     return;
   }
   size_t lds = (size_t(GQ) * a.d + size_t(GK) * (a.d + 1) + size_t(GK) * a.dv + size_t(GQ) * GK) * sizeof(float);

@@ -767,6 +767,34 @@ static bool spans_fit(const GemmArgs& a) {
   return a_span < lim && w_span < lim;
 }
 
+// The tile for an M x N x K product (batch of them): the one with the least
+// modelled time, rounds * (work per tile) / (rate per workgroup), where a
+// round is one workgroup on every slot (256 CUs x the workgroups one CU
+// holds) and a tile's work is BM * BN * (K + K0), K0 its fixed cost in
+// K-equivalents. Rates and K0 are fitted to a sweep of every tile over the
+// DiTs' and the UNet's GEMM shapes on MI355X (rows 154 to 13778, N 640 to
+// 12288, K 640 to 12288): within 0.2% of the best tile on average, 3.5% at
+// worst. Index 0..3: 256x256, 128x128, 64x128, 64x64.
+static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
+  struct Tile { int bm, bn, per_cu; double rate; double k0; };
+  static const Tile tiles[4] = {
+      {256, 256, 1, 1000.0, 512.0}, {128, 128, 2, 920.0, 128.0}, {64, 128, 3, 700.0, 128.0}, {64, 64, 4, 560.0, 128.0}};
+  int best = 0;
+  double best_t = 0;
+  for (int i = 0; i < 4; i++) {
+    const Tile& t = tiles[i];
+    const int64_t count = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
+    const int64_t slots = 256 * t.per_cu;
+    const int64_t rounds = (count + slots - 1) / slots;
+    const double time = double(rounds) * t.bm * t.bn * (double(K) + t.k0) * slots / t.rate;
+    if (i == 0 || time < best_t) {
+      best = i;
+      best_t = time;
+    }
+  }
+  return best;
+}
+
 static GemmKind choose(const GemmArgs& a) {
   const int MR = a.M;
   if (!w_aligned(a)) return K_GENERIC_LINEAR;
@@ -789,15 +817,10 @@ static GemmKind choose(const GemmArgs& a) {
       if (!strcmp(pin, "64x128lds") && a.w_dtype != NDX_I8) return K_LDS_64x128;
       if (!strcmp(pin, "64x64lds") && a.w_dtype != NDX_I8) return K_LDS_64x64;
     }
-    // The largest tile whose count still fills the 256 CUs well, fitted to
-    // a sweep of every tile over the MMDiT's GEMM shapes (rows 128 to
-    // 13778, N 3072/9216/12288, K 3072/12288) on MI355X.
-    auto tiles = [&](int bm, int bn) { return int64_t((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) * a.batch; };
-    const bool i8 = a.w_dtype == NDX_I8;
-    if (tiles(256, 256) >= 240) return i8 ? K_MFMA_256 : K_LDS_256;
-    if (tiles(128, 128) >= 700) return i8 ? K_MFMA_128 : K_LDS_128;
-    if (tiles(64, 128) >= 500) return i8 ? K_MFMA_64 : K_LDS_64x128;
-    return i8 ? K_MFMA_64x64 : K_LDS_64x64;
+    static const GemmKind lds[4] = {K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
+    static const GemmKind reg[4] = {K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64};
+    const int t = pick_tile(a.M, a.N, a.K, a.batch);
+    return a.w_dtype == NDX_I8 ? reg[t] : lds[t];
   }
   if (a.a_dtype == NDX_F32 && a.K % 8 == 0) return K_F32;
   return K_GENERIC_LINEAR;
@@ -889,11 +912,8 @@ static ConvKind conv_choose(const GemmArgs& g) {
     if (!strcmp(pin, "64x128")) return CK_64x128;
     if (!strcmp(pin, "64x64")) return CK_64x64;
   }
-  auto tiles = [&](int bm, int bn) { return int64_t((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch; };
-  if (g.M >= 256 && tiles(256, 256) >= 240) return CK_256;
-  if (g.M >= 128 && tiles(128, 128) >= 500) return CK_128;
-  if (tiles(64, 128) >= 500) return CK_64x128;
-  return CK_64x64;
+  static const ConvKind kinds[4] = {CK_256, CK_128, CK_64x128, CK_64x64};
+  return kinds[pick_tile(g.M, g.N, g.K, g.batch)];
 }
 
 static GemmArgs conv_gemm_args(const ConvArgs& c) {

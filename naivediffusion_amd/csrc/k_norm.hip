@@ -3,6 +3,8 @@
 // the per-head RMSNorm + rotate-half RoPE of the attention inputs, and
 // GroupNorm (+affine, +SiLU).
 
+#include <algorithm>
+
 #include "k_common.h"
 
 namespace ndx {
@@ -354,35 +356,123 @@ void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s) {
 // GroupNorm over NCHW: one 1024-thread block per (n, group), two passes for
 // the statistics (mean, then the centred sum of squares) and one for the
 // output with the per-channel affine and the optional SiLU.
-__global__ __launch_bounds__(1024) void group_norm_kernel(GroupNormArgs a) {
-  __shared__ float red[16];
-  const int n = blockIdx.x / a.groups, g = blockIdx.x % a.groups;
+// GroupNorm in two launches so every CU has work: `splits` workgroups per
+// (n, group) each reduce one contiguous chunk of the group to (count, mean,
+// M2) (two passes over the chunk, which stays in cache), then each
+// workgroup of the apply pass combines its group's partials (Chan et al.'s
+// pairwise update) and normalises one chunk, with the per-channel affine
+// and the optional SiLU.
+int group_norm_splits(int64_t count) {
+  int64_t s = (count + 8191) / 8192;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(s, 64));
+}
+
+// Chunk `split` of a group's count elements: a multiple of 4 long, so the
+// chunks keep the 4-element alignment of the group's start.
+__device__ __forceinline__ void gn_chunk(const GroupNormArgs& a, int64_t count, int split, int64_t& lo,
+                                         int64_t& hi) {
+  const int64_t per = ((count + a.splits - 1) / a.splits + 3) & ~int64_t(3);
+  lo = min(count, int64_t(split) * per);
+  hi = min(count, lo + per);
+}
+
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void group_norm_stats_kernel(GroupNormArgs a) {
+  __shared__ float red[4];
+  const int ng = blockIdx.x, split = blockIdx.y;
+  const int n = ng / a.groups, g = ng % a.groups;
   const int cpg = a.C / a.groups;
   const int64_t count = int64_t(cpg) * a.HW;
   const int64_t base = (int64_t(n) * a.C + int64_t(g) * cpg) * a.HW;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t lo, hi;
+  gn_chunk(a, count, split, lo, hi);
+  // Four elements per thread and step when the chunk and the rows allow
+  // 4-element vector access (a uniform choice).
+  const bool vec = (uintptr_t)a.x % 16 == 0 && ((base + lo) & 3) == 0 && ((hi - lo) & 3) == 0;
   float s = 0.f;
-  for (int64_t i = t; i < count; i += 1024) s += load_f(a.x, a.dtype, base + i);
-  s = wave_sum(s);
-  if (lane == 0) red[w] = s;
-  __syncthreads();
-  s = 0.f;
-  for (int k = 0; k < 16; k++) s += red[k];
-  const float mean = s / count;
-  __syncthreads();
-  float q = 0.f;
-  for (int64_t i = t; i < count; i += 1024) {
-    float d = load_f(a.x, a.dtype, base + i) - mean;
-    q += d * d;
+  if (vec) {
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 1024) {
+      const float4 v = load4(a.x, a.dtype, base + i);
+      s += (v.x + v.y) + (v.z + v.w);
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) s += load_f(a.x, a.dtype, base + i);
   }
-  q = wave_sum(q);
-  if (lane == 0) red[w] = q;
+  const float cnt = float(hi - lo);
+  const float mean = cnt > 0 ? block_sum_256(s, red) / cnt : 0.f;
+  float q = 0.f;
+  if (vec) {
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 1024) {
+      const float4 v = load4(a.x, a.dtype, base + i);
+      const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+      q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+      const float d = load_f(a.x, a.dtype, base + i) - mean;
+      q += d * d;
+    }
+  }
+  q = block_sum_256(q, red);
+  if (threadIdx.x == 0) {
+    float* p = a.partial + (int64_t(ng) * a.splits + split) * 3;
+    p[0] = cnt;
+    p[1] = mean;
+    p[2] = q;
+  }
+}
+
+__global__ __launch_bounds__(256) void group_norm_apply_kernel(GroupNormArgs a) {
+  __shared__ float stat[2];
+  const int ng = blockIdx.x, split = blockIdx.y;
+  const int n = ng / a.groups, g = ng % a.groups;
+  const int cpg = a.C / a.groups;
+  const int64_t count = int64_t(cpg) * a.HW;
+  const int64_t base = (int64_t(n) * a.C + int64_t(g) * cpg) * a.HW;
+  if (threadIdx.x == 0) {
+    const float* p = a.partial + int64_t(ng) * a.splits * 3;
+    float c = 0.f, mean = 0.f, m2 = 0.f;
+    for (int k = 0; k < a.splits; k++) {
+      const float cb = p[3 * k], mb = p[3 * k + 1], qb = p[3 * k + 2];
+      if (cb == 0.f) continue;
+      const float ct = c + cb, d = mb - mean;
+      mean += d * (cb / ct);
+      m2 += qb + d * d * (c * cb / ct);
+      c = ct;
+    }
+    stat[0] = mean;
+    stat[1] = 1.0f / sqrtf(m2 / c + a.eps);
+  }
   __syncthreads();
-  q = 0.f;
-  for (int k = 0; k < 16; k++) q += red[k];
-  const float rstd = 1.0f / sqrtf(q / count + a.eps);
-  for (int64_t i = t; i < count; i += 1024) {
-    int c = g * cpg + (int)(i / a.HW);
+  const float mean = stat[0], rstd = stat[1];
+  int64_t lo, hi;
+  gn_chunk(a, count, split, lo, hi);
+  // Vector path: 4 elements of one channel (HW a multiple of 4).
+  const bool vec = (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.y % 16 == 0 && ((base + lo) & 3) == 0 &&
+                   ((hi - lo) & 3) == 0 && (a.HW & 3) == 0;
+  if (vec) {
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 1024) {
+      const int c = g * cpg + (int)(i / a.HW);
+      const float w = a.weight ? load_f(a.weight, a.w_dtype, c) * rstd : rstd;
+      const float b = (a.bias ? load_f(a.bias, a.w_dtype, c) : 0.f) - mean * w;
+      const float4 v = load4(a.x, a.dtype, base + i);
+      float y[4] = {v.x * w + b, v.y * w + b, v.z * w + b, v.w * w + b};
+      if (a.silu)
+        for (int e = 0; e < 4; e++) y[e] = silu_f(y[e]);
+      store4(a.y, a.y_dtype, base + i, make_float4(y[0], y[1], y[2], y[3]));
+    }
+    return;
+  }
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+    const int c = g * cpg + (int)(i / a.HW);
     float y = (load_f(a.x, a.dtype, base + i) - mean) * rstd;
     if (a.weight) y *= load_f(a.weight, a.w_dtype, c);
     if (a.bias) y += load_f(a.bias, a.w_dtype, c);
@@ -392,7 +482,9 @@ __global__ __launch_bounds__(1024) void group_norm_kernel(GroupNormArgs a) {
 }
 
 void launch_group_norm(const GroupNormArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(group_norm_kernel, dim3(a.N * a.groups), dim3(1024), 0, s, a);
+  dim3 g(a.N * a.groups, a.splits);
+  hipLaunchKernelGGL(group_norm_stats_kernel, g, dim3(256), 0, s, a);
+  hipLaunchKernelGGL(group_norm_apply_kernel, g, dim3(256), 0, s, a);
 }
 
 }  // namespace ndx

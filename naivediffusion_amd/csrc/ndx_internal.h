@@ -140,7 +140,12 @@ struct GroupNormArgs {
   const void* weight; const void* bias; int w_dtype;
   float eps;
   int silu;
+  // Split statistics: `splits` workgroups per (n, group) each leave (count,
+  // mean, M2) in `partial` (N * groups * splits * 3 floats of scratch).
+  float* partial; int splits;
 };
+// The split count the group norm uses for a shape, and its scratch bytes.
+int group_norm_splits(int64_t count);
 
 struct ConvArgs {
   const void* x; int x_dtype;  // [N, Cin, H, W] packed

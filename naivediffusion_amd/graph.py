@@ -201,6 +201,9 @@ class Ops:
 
     @staticmethod
     def Slice(x, offsets, sizes, strides=None):
+        rank = len(x.Shape)
+        if len(offsets) != rank or len(sizes) != rank or (strides is not None and len(strides) != rank):
+            raise _lib.ArgumentError(f"a slice of a rank-{rank} tensor takes {rank} offsets, sizes and strides")
         st = None if strides is None else _lib.shape_array(strides)
         return x.graph._new("ndx_op_slice", x.id, _lib.shape_array(offsets), _lib.shape_array(sizes), st)
 

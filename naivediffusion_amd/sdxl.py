@@ -168,6 +168,18 @@ def synthetic_weights(cfg: SdxlConfig, seed: int, dtype: HostDataType = HostData
     return out
 
 
+def device_weights(device: Device, cfg: SdxlConfig, seed: int, dtype: HostDataType = HostDataType.Float16) -> dict:
+    """Synthetic weights made on the GPU at `dtype`: N(0, 0.02) everywhere
+    but the norm weights, which are 1."""
+    out = {}
+    for name, shape in weight_shapes(cfg).items():
+        if (".norm" in name or name.startswith("conv_norm_out")) and name.endswith("weight"):
+            out[name] = device.Upload(HostTensor.FromFloats(np.ones(shape, np.float32)).ConvertTo(dtype))
+        else:
+            out[name] = device.Normal(dtype, shape, rng.tensor_seed(seed, name), 0.0, 0.02)
+    return out
+
+
 def timestep_embedding(timesteps: Sequence[float], dim: int, max_period: float = 10000.0) -> np.ndarray:
     """UNetModel.TimestepEmbedding (:150-169): per timestep, cosines of
     t * exp(-ln(max_period) i / half) then sines (flip_sin_to_cos), computed

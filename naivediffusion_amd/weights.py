@@ -21,8 +21,7 @@ def device_stack(device: Device, tensors, columns: int = 0) -> DeviceTensor:
     ins = [g.Input(t.DataType, list(t.Shape)) for t in tensors]
     if columns:
         rows = tensors[0].Shape[0]
-        out = Ops.Reinterpret(Ops.Identity(Ops.Slice(ins[0], [0, 0, 0, 0], [1, 1, rows, columns])),
-                              [rows, columns])
+        out = Ops.Identity(Ops.Slice(ins[0], [0, 0], [rows, columns]))
     else:
         joined = Ops.Join([Ops.Reinterpret(e, [1, 1] + list(e.Shape)) for e in ins], 2)
         out = Ops.Reinterpret(joined, list(joined.Shape[2:]))

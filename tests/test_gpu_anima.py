@@ -99,3 +99,20 @@ def test_anima_patch_layouts_bit_exact(device):
                        HostTensor.FromFloats(tok.reshape(1, 1, -1, C * 4))])
     assert np.array_equal(p.ToFloats().reshape(tok.shape), oracle.anima_patchify(latent))
     assert np.array_equal(u.ToFloats().reshape(C, H, W), oracle.anima_unpatchify(tok, C, H, W))
+
+
+def test_anima_device_weights_match_host_weights(device):
+    """Weights made on the device (stacked and column-sliced there) give the
+    same step, bit for bit, as the same values passed from the host."""
+    cfg = NARROW
+    lat, n_ctx = 8, 16
+    dw = anima.device_weights(device, cfg, 13, DT.BFloat16)
+    hw = {k: t.Download().ToFloats().reshape(t.Shape) for k, t in dw.items()}
+    latent = normal("dl", (cfg.latent_channels, lat, lat))
+    ctx = normal("dc", (n_ctx, cfg.context_width))
+    outs = []
+    for w in (dw, hw):
+        den = anima.AnimaDit(device, cfg, w, lat * 8, lat * 8, n_ctx, DT.BFloat16)
+        outs.append(den.Predict(HostTensor.FromFloats(latent), 500.0, 0.4, {"context": ctx}).ToFloats())
+        den.Dispose()
+    assert np.array_equal(outs[0], outs[1])

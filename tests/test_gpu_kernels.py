@@ -108,8 +108,9 @@ def test_linear_tile_configurations(device, M, K, N, B, int8):
 
 
 def test_tile_cases_reached_every_configuration():
-    assert SEEN_FAMILIES >= {"gemm_mfma_256x256", "gemm_mfma_128x128", "gemm_mfma_64x128", "gemm_mfma_64x64",
-                             "gemv"}, SEEN_FAMILIES
+    # The 256x256 tile wins only at the step's own sizes (5376 rows, K 12288):
+    # it is covered pinned, below, and by the step tests.
+    assert SEEN_FAMILIES >= {"gemm_mfma_128x128", "gemm_mfma_64x128", "gemm_mfma_64x64", "gemv"}, SEEN_FAMILIES
 
 
 @pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64", "256lds", "128lds", "64x128lds", "64x64lds"])
@@ -203,6 +204,8 @@ def test_device_quantizer_is_bit_exact_with_the_oracle(device):
     (130, 517, 4, 128, DT.BFloat16),
     (257, 257, 2, 128, DT.Float32),
     (64, 100, 3, 64, DT.Float32),
+    (1500, 1433, 3, 128, DT.Float32),
+    (129, 4096, 2, 64, DT.Float32),
 ])
 def test_attention_against_oracle(device, T, S, H, d, dtype):
     print(f"[gpu] attention T={T} S={S} H={H} d={d} {dtype.name}", flush=True)
@@ -240,20 +243,24 @@ def test_attention_masks(device, dtype):
     assert rel_err(o2.reshape(1, T, -1), oracle.mha(q, k, v, H, mask_kind=2, mask=table)) <= tol
 
 
-def test_attention_reads_joined_streams_in_place(device):
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float32])
+def test_attention_reads_joined_streams_in_place(device, dtype):
     """A join of the image and text rows feeding the attention is read as
-    two row segments; the result equals attention over the packed join."""
+    two row segments; the result equals attention over the packed join.
+    Scores spread wide (x3) so the running max moves across key tiles."""
     ni, nt, H, d = 300, 45, 4, 128
-    parts = {n: bf(normal(n, (1, 1, r, H * d))) for n, r in
+    parts = {n: bf(normal(n, (1, 1, r, H * d), 3.0 if n[0] == "q" else 1.0)) for n, r in
              (("qi", ni), ("qt", nt), ("ki", ni), ("kt", nt), ("vi", ni), ("vt", nt))}
-    model = nd.ModelBuilder(device, DT.BFloat16)
+    model = nd.ModelBuilder(device, dtype)
     ph = {n: model.Placeholder(list(a.shape)) for n, a in parts.items()}
     j = [Ops.Join([ph[a], ph[b]], 2) for a, b in (("qi", "qt"), ("ki", "kt"), ("vi", "vt"))]
     model.Compile([Layers.Attend(*j, H)])
-    out = run(model, *[HostTensor.FromFloats(a).ConvertTo(DT.BFloat16) for a in parts.values()])[0]
+    out = run(model, *[HostTensor.FromFloats(a).ConvertTo(dtype) for a in parts.values()])[0]
     cat = [np.concatenate([parts[a], parts[b]], 2).reshape(1, ni + nt, H * d)
            for a, b in (("qi", "qt"), ("ki", "kt"), ("vi", "vt"))]
-    assert rel_err(out.reshape(1, ni + nt, -1), oracle.mha(*cat, H)) <= BF16_TOL
+    err = rel_err(out.reshape(1, ni + nt, -1), oracle.mha(*cat, H))
+    print(f"[gpu]   joined attention {dtype.name} rel err {err:.2e}", flush=True)
+    assert err <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
 
 
 # ---- norms ------------------------------------------------------------------------------
@@ -468,3 +475,28 @@ def test_errors_leave_the_device_usable(device):
         model.Run()
     with pytest.raises(nd.ArgumentError):
         model.Compiled.DispatchOnDevice([device.Upload(HostTensor.FromFloats(np.zeros(3, np.float32)))])
+
+
+@pytest.mark.parametrize("shape,groups", [((2, 320, 64, 64), 32), ((2, 1920, 32, 32), 32), ((1, 64, 7, 9), 32),
+                                          ((2, 640, 33, 31), 32), ((1, 32, 256, 256), 4)])
+@pytest.mark.parametrize("dtype,silu", [(DT.Float16, True), (DT.BFloat16, False), (DT.Float32, True)])
+def test_group_norm_split_statistics(device, shape, groups, dtype, silu):
+    """Layers.GroupNorm (+ SiLU) at SDXL's shapes: the statistics split over
+    many workgroups per group, ragged extents that take the scalar paths, and
+    groups large enough to need every split."""
+    print(f"[gpu] group norm {shape} g={groups} {dtype.name} silu={silu}", flush=True)
+    x = normal("gx", shape) * 2.0 + 0.5
+    c = shape[1]
+    w = 1.0 + normal("gw", (c,), 0.2)
+    b = normal("gb", (c,), 0.2)
+    xin = HostTensor.FromFloats(x).ConvertTo(dtype)
+    xr = xin.ToFloats().reshape(shape)
+    model = nd.ModelBuilder(device, dtype)
+    p = model.Placeholder(list(shape), dtype)
+    model.Compile([Layers.GroupNorm(model, p, HostTensor.FromFloats(w), HostTensor.FromFloats(b), groups, 1e-5,
+                                    silu=silu)])
+    out = run(model, xin)[0]
+    wd = HostTensor.FromFloats(w).ConvertTo(dtype).ToFloats()
+    bd = HostTensor.FromFloats(b).ConvertTo(dtype).ToFloats()
+    ref = oracle.group_norm(xr, groups, wd, bd, 1e-5, silu)
+    assert rel_err(out.reshape(shape), ref) <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
