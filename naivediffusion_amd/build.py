@@ -29,6 +29,10 @@ HIPCC_FLAGS = [
     "-fvisibility=hidden",
     # Packed fp32 instructions stay off: hipcc emits ordinary scalar fp32.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Small per-thread arrays (staged tile chunks) stay in registers: every
+    # kernel here manages its LDS explicitly, and an array moved into LDS
+    # costs a workgroup slot per CU and extra LDS traffic.
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wno-unused-result",
 ]
 

@@ -1235,12 +1235,19 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
           if (!w.quant && w.v.size[3] > 1 && w.v.stride[3] != 1) n.in[1] = c.pack(n.in[1], sched);
         }
         break;
-      case OP_ATTN:
+      case OP_ATTN: {
         for (int j = 0; j < 3; j++) {
           if (n.seg[j][1] >= 0) continue;
           ensure_rows(n.seg[j][0]);
         }
+        const View4& qv = c.values[n.in[0]].v;
+        const View4& kv = c.values[n.in[1]].v;
+        const View4& vv = c.values[n.in[2]].v;
+        n.scratch_bytes = attention_scratch_bytes((int)(qv.size[0] * qv.size[1]), (int)qv.size[2], (int)kv.size[2], n.i0,
+                                                  (int)(qv.size[3] / n.i0), (int)(vv.size[3] / n.i0),
+                                                  c.values[n.in[0]].dtype);
         break;
+      }
       case OP_HNR:
         ensure_rows(n.in[0]);
         ensure_packed(n.in[1]);
@@ -1575,7 +1582,7 @@ struct Runner {
           // [b, h, t, s] strides; a size-1 axis broadcasts.
           for (int i = 0; i < 4; i++) a.mask_stride[i] = mk.v.size[i] == 1 ? 0 : mk.v.stride[i];
         }
-        launch_attention(a, s);
+        launch_attention(a, n.scratch_bytes > 0 ? (char*)m->arena + n.scratch_off : nullptr, s);
         break;
       }
       case OP_HNR: {

@@ -2,7 +2,7 @@
 // [B, T, H*d] rows, the semantics of DmlOps.MultiheadAttention
 // (Dml/DmlOps.cs:480-520; a ruled-out score gets -10000 added, :483).
 //
-// flash_attn_kernel (bf16 / f16, d = 64 or 128): a workgroup of 4 waves takes
+// flash_attn_kernel (bf16 / f16, d = 64 or 128): a tile of 4 waves takes
 // 128 queries of one (batch, head); each wave owns 32 queries. Scores are
 // computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16: lane l then holds
 // column l % 32 of S^T, i.e. one query, so the running max, the rescale of
@@ -20,6 +20,7 @@
 // attn_generic_kernel: any float type and head size, fp32 arithmetic with
 // expf; the path for odd shapes.
 
+#include <algorithm>
 #include <cstdlib>
 
 #include "k_common.h"
@@ -69,37 +70,34 @@ __device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// QT query tiles of 32 per wave: every K and V fragment read from LDS feeds
-// QT MFMAs. QT = 1 keeps the register file under 256 (two waves per SIMD);
-// QT = 2 halves the LDS traffic per MFMA at one wave per SIMD.
-template <typename T, int D, int MASK, int QT>
-__global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnArgs a, int grid) {
+// One tile: 128 queries (4 waves x 32) of one (batch, head) over key blocks
+// [kb0, kb1) of 64 keys. With part == nullptr the tile covers every key and
+// writes the normalised output; otherwise it leaves its unnormalised O^T
+// registers, running max and partial row sum in `part` (field-major, one
+// float per thread per field) for attn_combine_kernel.
+template <typename T, int D, int MASK>
+__device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int head, int b, int kb0, int kb1,
+                                               float* part, T (*Ks)[64 * D], T (*Vt)[D * 64]) {
   typedef typename AMfma<T>::V V;
-  constexpr int BQ = 128 * QT, BKEY = 64;
+  constexpr int BQ = 128, BKEY = 64;
   constexpr int KCH = D / 8;                      // 16-byte chunks per key row
   constexpr int KMASK = (KCH < 16 ? KCH : 16) - 1;
   constexpr int K_PER = BKEY * KCH / 256;         // K chunks per thread
   constexpr int V_TASKS = (BKEY / 4) * (D / 8);   // (4-key group, 8-d chunk) tasks
   constexpr int DT = D / 32;                      // output tiles along d
-  __shared__ __attribute__((aligned(16))) T Ks[2][BKEY * D];
-  __shared__ __attribute__((aligned(16))) T Vt[2][D * BKEY];
 
-  int qb, head, b;
-  if (!attn_tile(blockIdx.x, grid, (a.T + BQ - 1) / BQ, a.H, a.B, qb, head, b)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lq = lane & 31, lh = lane >> 5;
   const int64_t col0 = int64_t(head) * D;
-  int qi[QT];
-#pragma unroll
-  for (int t = 0; t < QT; t++) qi[t] = qb * BQ + (wave * QT + t) * 32 + lq;
+  const int qi = qb * BQ + wave * 32 + lq;
+  const int qm = min(qi, a.T - 1);
 
   // Q^T fragments, resident for the whole key loop.
-  V qf[QT][D / 16];
+  V qf[D / 16];
+  {
+    const T* qrow = seg_row<T>(a.q, b, qm) + col0;
 #pragma unroll
-  for (int t = 0; t < QT; t++) {
-    const T* qrow = seg_row<T>(a.q, b, min(qi[t], a.T - 1)) + col0;
-#pragma unroll
-    for (int s = 0; s < D / 16; s++) qf[t][s] = *(const V*)(qrow + s * 16 + lh * 8);
+    for (int s = 0; s < D / 16; s++) qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
   }
 
   uint4 rk[K_PER];
@@ -132,10 +130,10 @@ __global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnAr
       *(uint4*)&Ks[buf][key * D + ((c ^ (key & KMASK)) << 3)] = rk[i];
     }
     if (tid < V_TASKS) {
-      const uint32_t* w0 = (const uint32_t*)&rv[0];
-      const uint32_t* w1 = (const uint32_t*)&rv[1];
-      const uint32_t* w2 = (const uint32_t*)&rv[2];
-      const uint32_t* w3 = (const uint32_t*)&rv[3];
+      const uint32_t w0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+      const uint32_t w1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+      const uint32_t w2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
+      const uint32_t w3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         // Two d rows per 32-bit word: (d, d+1) of keys 4g..4g+3.
@@ -150,39 +148,29 @@ __global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnAr
     }
   };
 
-  f32x16 o[QT][DT];
+  f32x16 o[DT];
 #pragma unroll
-  for (int t = 0; t < QT; t++)
+  for (int j = 0; j < DT; j++)
 #pragma unroll
-    for (int j = 0; j < DT; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) o[t][j][r] = 0.f;
-  float m_run[QT], l_part[QT];
-#pragma unroll
-  for (int t = 0; t < QT; t++) {
-    m_run[t] = -INFINITY;
-    l_part[t] = 0.f;
-  }
+    for (int r = 0; r < 16; r++) o[j][r] = 0.f;
+  float m_run = -INFINITY, l_part = 0.f;
   const float sl = a.scale * kLog2e;
   const float mask_add = -10000.0f * kLog2e;
   const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
 
-  const int KB = (a.S + BKEY - 1) / BKEY;
-  load_kv(0);
+  load_kv(kb0);
   store_kv(0);
   __syncthreads();
-  for (int kb = 0; kb < KB; kb++) {
-    const int cur = kb & 1;
-    if (kb + 1 < KB) load_kv(kb + 1);
+  for (int kb = kb0; kb < kb1; kb++) {
+    const int cur = (kb - kb0) & 1;
+    if (kb + 1 < kb1) load_kv(kb + 1);
 
-    // S^T for 64 keys: two 32-key tiles per query tile.
-    f32x16 sacc[QT][2];
+    // S^T for 64 keys: two 32-key tiles.
+    f32x16 sacc[2];
 #pragma unroll
-    for (int t = 0; t < QT; t++)
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) sacc[t][kt][r] = 0.f;
+      for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       const int key = kt * 32 + lq;
@@ -190,67 +178,58 @@ __global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnAr
       for (int s = 0; s < D / 16; s++) {
         const int c = 2 * s + lh;
         const V kf = *(const V*)&Ks[cur][key * D + ((c ^ (key & KMASK)) << 3)];
-#pragma unroll
-        for (int t = 0; t < QT; t++) sacc[t][kt] = AMfma<T>::mma(kf, qf[t][s], sacc[t][kt]);
+        sacc[kt] = AMfma<T>::mma(kf, qf[s], sacc[kt]);
       }
     }
     // Scale (into log2 units), mask, running max. The key tail is only
     // checked in the last block.
     const bool tail = (kb + 1) * BKEY > a.S;
+    float mloc = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < QT; t++) {
-      const int qm = min(qi[t], a.T - 1);
-      float mloc = -INFINITY;
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          float x = sacc[t][kt][r] * sl;
-          const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (MASK == NDX_MASK_KEY_LENGTH) {
-            if (key >= key_len) x += mask_add;
-          } else if (MASK == NDX_MASK_BOOLEAN) {
-            const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
-                               int64_t(min(key, a.S - 1)) * a.mask_stride[3];
-            if (a.mask[mi] == 0) x += mask_add;
-          }
-          if (tail && key >= a.S) x = -INFINITY;
-          sacc[t][kt][r] = x;
-          mloc = fmaxf(mloc, x);
+      for (int r = 0; r < 16; r++) {
+        float x = sacc[kt][r] * sl;
+        const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (MASK == NDX_MASK_KEY_LENGTH) {
+          if (key >= key_len) x += mask_add;
+        } else if (MASK == NDX_MASK_BOOLEAN) {
+          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
+                             int64_t(min(key, a.S - 1)) * a.mask_stride[3];
+          if (a.mask[mi] == 0) x += mask_add;
         }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float m_new = fmaxf(m_run[t], mloc);
-      // Rescale the running output only when some lane's max moved: after
-      // the first blocks the maxima settle and the multiply is skipped.
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run[t])) {
-        const float alpha = exp2f(m_run[t] - m_new);
-        l_part[t] *= alpha;
-#pragma unroll
-        for (int j = 0; j < DT; j++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) o[t][j][r] *= alpha;
+        if (tail && key >= a.S) x = -INFINITY;
+        sacc[kt][r] = x;
+        mloc = fmaxf(mloc, x);
       }
-      m_run[t] = m_new;
-      float psum = 0.f;
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    // Rescale the running output only when some lane's max moved: after
+    // the first blocks the maxima settle and the multiply is skipped.
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+      const float alpha = exp2f(m_run - m_new);
+      l_part *= alpha;
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++)
+      for (int j = 0; j < DT; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float p = exp2f(sacc[t][kt][r] - m_new);
-          sacc[t][kt][r] = p;
-          psum += p;
-        }
-      l_part[t] += psum;
+        for (int r = 0; r < 16; r++) o[j][r] *= alpha;
     }
+    m_run = m_new;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float p = exp2f(sacc[kt][r] - m_new);
+        sacc[kt][r] = p;
+        l_part += p;
+      }
 
     // O^T += V^T P^T over four 16-key steps.
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      V pb[QT];
+      V pb;
 #pragma unroll
-      for (int t = 0; t < QT; t++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) pb[t][j] = (T)sacc[t][u >> 1][(u & 1) * 8 + j];
+      for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) {
         const int d = dt * 32 + lq;
@@ -258,30 +237,124 @@ __global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void flash_attn_kernel(AttnAr
         const uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
         const uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
         const V vf = __builtin_bit_cast(V, make_uint4(x1.x, x1.y, x2.x, x2.y));
-#pragma unroll
-        for (int t = 0; t < QT; t++) o[t][dt] = AMfma<T>::mma(vf, pb[t], o[t][dt]);
+        o[dt] = AMfma<T>::mma(vf, pb, o[dt]);
       }
     }
-    if (kb + 1 < KB) store_kv(cur ^ 1);
+    if (kb + 1 < kb1) store_kv(cur ^ 1);
     __syncthreads();
   }
 
+  if (part) {
 #pragma unroll
-  for (int t = 0; t < QT; t++) {
-    const float l_tot = l_part[t] + __shfl_xor(l_part[t], 32, 64);
-    const float inv = 1.0f / l_tot;
-    if (qi[t] < a.T) {
-      T* orow = (T*)out_row(a, b, qi[t], sizeof(T)) + col0;
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++)
+      for (int r = 0; r < 16; r++) part[(dt * 16 + r) * 256 + tid] = o[dt][r];
+    part[DT * 16 * 256 + tid] = m_run;
+    part[(DT * 16 + 1) * 256 + tid] = l_part;
+    return;
+  }
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if (qi < a.T) {
+    T* orow = (T*)out_row(a, b, qi, sizeof(T)) + col0;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int d = dt * 32 + 8 * g + 4 * lh;
-          T v4[4];
+    for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) v4[e] = (T)(o[t][dt][g * 4 + e] * inv);
-          *(uint2*)(orow + d) = *(const uint2*)v4;
-        }
+      for (int g = 0; g < 4; g++) {
+        const int d = dt * 32 + 8 * g + 4 * lh;
+        T v4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v4[e] = (T)(o[dt][g * 4 + e] * inv);
+        *(uint2*)(orow + d) = *(const uint2*)v4;
+      }
+  }
+}
+
+// How tiles are spread over workgroups. Without `split` there is one tile
+// per workgroup (decoded XCD-aware by attn_tile). With it the grid is the
+// head_tiles whole tiles (a whole number of rounds of the resident
+// workgroups), then `ps` pieces of each of the tail_tiles remaining tiles,
+// piece k taking key blocks [k KB / ps, (k + 1) KB / ps): the dispatcher
+// starts them in order, so the last round is short pieces instead of a few
+// whole tiles. A piece leaves its partial in `part`; attn_combine_kernel
+// merges the ps partials of each tail tile.
+struct AttnSched {
+  int grid;
+  int split;
+  int qblocks, KB;
+  int head_tiles, tail_tiles, ps;
+  float* part;
+};
+
+__device__ __forceinline__ void decode_tile(int t, int qblocks, int H, int& qb, int& head, int& b) {
+  qb = t % qblocks;
+  const int r = t / qblocks;
+  head = r % H;
+  b = r / H;
+}
+
+template <typename T, int D, int MASK>
+__global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, AttnSched sc) {
+  constexpr int DT = D / 32;
+  __shared__ __attribute__((aligned(16))) T Ks[2][64 * D];
+  __shared__ __attribute__((aligned(16))) T Vt[2][D * 64];
+  int qb, head, b;
+  if (!sc.split) {
+    if (!attn_tile(blockIdx.x, sc.grid, sc.qblocks, a.H, a.B, qb, head, b)) return;
+    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, Ks, Vt);
+    return;
+  }
+  const int w = blockIdx.x;
+  if (w < sc.head_tiles) {
+    // Consecutive tiles (the query blocks of one head) to one XCD.
+    const int t = (w % 8) * (sc.head_tiles / 8) + w / 8;
+    decode_tile(t, sc.qblocks, a.H, qb, head, b);
+    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, Ks, Vt);
+    return;
+  }
+  const int p = w - sc.head_tiles;
+  const int ti = p / sc.ps, k = p % sc.ps;
+  decode_tile(sc.head_tiles + ti, sc.qblocks, a.H, qb, head, b);
+  attn_tile_body<T, D, MASK>(a, qb, head, b, k * sc.KB / sc.ps, (k + 1) * sc.KB / sc.ps,
+                             sc.part + int64_t(p) * ((DT * 16 + 2) * 256), Ks, Vt);
+}
+
+// Merges the ps partials of tail tile blockIdx.x, columns d in [32 y,
+// 32 y + 32) with y = blockIdx.y: each piece left O^T, the running max and
+// the partial row sum in the same lane layout, so each thread combines its
+// own registers; the maxima and sums first (two loads per piece), then the
+// 16 outputs of its column group (all loads independent).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, AttnSched sc) {
+  constexpr int F = D / 32 * 16;
+  const int ti = blockIdx.x, dt = blockIdx.y, tid = threadIdx.x;
+  const float* base = sc.part + int64_t(ti) * sc.ps * ((F + 2) * 256);
+  float m = -INFINITY;
+  for (int k = 0; k < sc.ps; k++) m = fmaxf(m, base[int64_t(k) * (F + 2) * 256 + F * 256 + tid]);
+  float l = 0.f, o[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) o[r] = 0.f;
+  for (int k = 0; k < sc.ps; k++) {
+    const float* part = base + int64_t(k) * (F + 2) * 256;
+    const float w = exp2f(part[F * 256 + tid] - m);
+    l += part[(F + 1) * 256 + tid] * w;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] += part[(dt * 16 + r) * 256 + tid] * w;
+  }
+  int qb, head, b;
+  decode_tile(sc.head_tiles + ti, sc.qblocks, a.H, qb, head, b);
+  const int lane = tid & 63, wave = tid >> 6, lq = lane & 31, lh = lane >> 5;
+  const int qi = qb * 128 + wave * 32 + lq;
+  const float inv = 1.0f / (l + __shfl_xor(l, 32, 64));
+  if (qi < a.T) {
+    T* orow = (T*)out_row(a, b, qi, sizeof(T)) + int64_t(head) * D;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = dt * 32 + 8 * g + 4 * lh;
+      T v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) v4[e] = (T)(o[g * 4 + e] * inv);
+      *(uint2*)(orow + d) = *(const uint2*)v4;
     }
   }
 }
@@ -547,44 +620,93 @@ static bool rows_aligned(const AttnSeg& s, int esize) {
   return true;
 }
 
-void launch_attention(const AttnArgs& a, hipStream_t s) {
+static int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) ==
+                                                 hipSuccess && c > 0)
+      n = c;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+// The schedule of the 16-bit flash kernel for a shape: split when at least
+// one full round of whole tiles leaves a last round at most three quarters
+// full (two resident workgroups per CU); the tail tiles are cut into as
+// many pieces as fill one round, at most 8 (the pieces' own overhead and
+// the merge grow with their count) and at least 2 key blocks each.
+static AttnSched attn_schedule(int B, int T, int S, int H) {
+  AttnSched sc{};
+  sc.qblocks = (T + 127) / 128;
+  sc.KB = (S + 63) / 64;
+  const int tiles = sc.qblocks * H * B;
+  const int slots = cu_count() * 2;
+  const int full = tiles / slots, tail = tiles - full * slots;
+  const int ps = std::min(std::min((slots + tail - 1) / std::max(tail, 1), 8), sc.KB / 2);
+  if (full >= 1 && tail > 0 && tail * 4 <= slots * 3 && ps >= 2 && slots % 8 == 0) {
+    sc.split = 1;
+    sc.head_tiles = full * slots;
+    sc.tail_tiles = tail;
+    sc.ps = ps;
+    sc.grid = sc.head_tiles + tail * ps;
+  } else {
+    sc.grid = (tiles + 7) / 8 * 8;
+  }
+  return sc;
+}
+
+static bool attn_mfma16(int dtype, int d, int dv) {
+  return (dtype == NDX_BF16 || dtype == NDX_F16) && d == dv && (d == 128 || d == 64);
+}
+
+int64_t attention_scratch_bytes(int B, int T, int S, int H, int d, int dv, int dtype) {
+  if (T == 0 || B == 0 || !attn_mfma16(dtype, d, dv)) return 0;
+  const AttnSched sc = attn_schedule(B, T, S, H);
+  if (!sc.split) return 0;
+  return int64_t(sc.tail_tiles) * sc.ps * (d / 32 * 16 + 2) * 256 * int64_t(sizeof(float));
+}
+
+void launch_attention(const AttnArgs& a, void* scratch, hipStream_t s) {
   if (a.T == 0 || a.B == 0) return;
-  const bool mfma = (a.dtype == NDX_BF16 || a.dtype == NDX_F16) && a.d == a.dv && (a.d == 128 || a.d == 64) &&
-                    rows_aligned(a.q, 2) && rows_aligned(a.k, 2) && rows_aligned(a.v, 2) &&
-                    (uintptr_t)a.out[0] % 16 == 0 && (uintptr_t)a.out[1] % 16 == 0;
+  const bool mfma = attn_mfma16(a.dtype, a.d, a.dv) && rows_aligned(a.q, 2) && rows_aligned(a.k, 2) &&
+                    rows_aligned(a.v, 2) && (uintptr_t)a.out[0] % 16 == 0 && (uintptr_t)a.out[1] % 16 == 0;
   if (mfma) {
-    // NDX_ATTN_QT=1|2 pins the query tiles per wave (for sweeps).
-    const char* pin = getenv("NDX_ATTN_QT");
-    int qt = pin ? atoi(pin) : 1;
-    if (qt != 2 || a.d != 128) qt = 1;
-    const int qblocks = (a.T + 128 * qt - 1) / (128 * qt);
-    const int grid = (qblocks * a.H * a.B + 7) / 8 * 8;
+    AttnSched sc = attn_schedule(a.B, a.T, a.S, a.H);
+    // NDX_ATTN_SPLIT=0 runs one whole tile per workgroup (for sweeps); read per launch.
+    const char* pin = getenv("NDX_ATTN_SPLIT");
+    if (pin && pin[0] == '0') scratch = nullptr;
+    if (sc.split && !scratch) sc = AttnSched{(sc.qblocks * a.H * a.B + 7) / 8 * 8, 0, sc.qblocks, sc.KB, 0, 0, 0, nullptr};
+    sc.part = (float*)scratch;
     const bool bf = a.dtype == NDX_BF16;
-#define NDX_FA(TYPE, DIM, MK, QT) \
-  hipLaunchKernelGGL((flash_attn_kernel<TYPE, DIM, MK, QT>), dim3(grid), dim3(256), 0, s, a, grid)
-#define NDX_FA_MASKS(TYPE, DIM, QT)                                      \
-  do {                                                                   \
-    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA(TYPE, DIM, 1, QT);    \
-    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA(TYPE, DIM, 2, QT);  \
-    else NDX_FA(TYPE, DIM, 0, QT);                                       \
+#define NDX_FA(TYPE, DIM, MK) \
+  hipLaunchKernelGGL((flash_attn_kernel<TYPE, DIM, MK>), dim3(sc.grid), dim3(256), 0, s, a, sc)
+#define NDX_FA_MASKS(TYPE, DIM)                                      \
+  do {                                                               \
+    if (a.mask_kind == NDX_MASK_KEY_LENGTH) NDX_FA(TYPE, DIM, 1);    \
+    else if (a.mask_kind == NDX_MASK_BOOLEAN) NDX_FA(TYPE, DIM, 2);  \
+    else NDX_FA(TYPE, DIM, 0);                                       \
   } while (0)
     if (bf) {
-      if (a.d == 128) {
-        if (qt == 2) NDX_FA_MASKS(__bf16, 128, 2);
-        else NDX_FA_MASKS(__bf16, 128, 1);
-      } else {
-        NDX_FA_MASKS(__bf16, 64, 1);
-      }
+      if (a.d == 128) NDX_FA_MASKS(__bf16, 128);
+      else NDX_FA_MASKS(__bf16, 64);
     } else {
-      if (a.d == 128) {
-        if (qt == 2) NDX_FA_MASKS(_Float16, 128, 2);
-        else NDX_FA_MASKS(_Float16, 128, 1);
-      } else {
-        NDX_FA_MASKS(_Float16, 64, 1);
-      }
+      if (a.d == 128) NDX_FA_MASKS(_Float16, 128);
+      else NDX_FA_MASKS(_Float16, 64);
     }
 #undef NDX_FA_MASKS
 #undef NDX_FA
+    if (sc.split) {
+      if (bf) {
+        if (a.d == 128) hipLaunchKernelGGL((attn_combine_kernel<__bf16, 128>), dim3(sc.tail_tiles, 128 / 32), dim3(256), 0, s, a, sc);
+        else hipLaunchKernelGGL((attn_combine_kernel<__bf16, 64>), dim3(sc.tail_tiles, 64 / 32), dim3(256), 0, s, a, sc);
+      } else {
+        if (a.d == 128) hipLaunchKernelGGL((attn_combine_kernel<_Float16, 128>), dim3(sc.tail_tiles, 128 / 32), dim3(256), 0, s, a, sc);
+        else hipLaunchKernelGGL((attn_combine_kernel<_Float16, 64>), dim3(sc.tail_tiles, 64 / 32), dim3(256), 0, s, a, sc);
+      }
+    }
     return;
   }
   const bool mfma32 = a.dtype == NDX_F32 && a.d == a.dv && (a.d == 128 || a.d == 64) && rows_aligned(a.q, 4) &&

@@ -187,7 +187,10 @@ struct PatchArgs {
 
 void launch_gemm(const GemmArgs& a, hipStream_t s);
 void launch_gemm_generic(const GemmGenericArgs& a, hipStream_t s);
-void launch_attention(const AttnArgs& a, hipStream_t s);
+// Attention; `scratch` holds attention_scratch_bytes(...) bytes (the split
+// schedule's partials), or is null to run without the split.
+void launch_attention(const AttnArgs& a, void* scratch, hipStream_t s);
+int64_t attention_scratch_bytes(int B, int T, int S, int H, int d, int dv, int dtype);
 void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s);
 void launch_row_norm(const RowNormArgs& a, hipStream_t s);
 void launch_group_norm(const GroupNormArgs& a, hipStream_t s);

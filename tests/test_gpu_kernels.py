@@ -500,3 +500,43 @@ def test_group_norm_split_statistics(device, shape, groups, dtype, silu):
     bd = HostTensor.FromFloats(b).ConvertTo(dtype).ToFloats()
     ref = oracle.group_norm(xr, groups, wd, bd, 1e-5, silu)
     assert rel_err(out.reshape(shape), ref) <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
+
+
+@pytest.mark.parametrize("B,T,S,H,d,mask", [
+    (4, 1100, 300, 16, 128, None),     # 576 tiles on 512 slots: one round whole, 64 tiles split by keys
+    (4, 1100, 300, 16, 128, "length"),
+    (2, 2100, 260, 16, 64, None),      # 544 tiles, d 64
+    (2, 2100, 517, 16, 64, "table"),
+    (3, 1500, 1111, 15, 128, None),    # 540 tiles, 18 key blocks
+])
+def test_attention_split_schedule(device, B, T, S, H, d, mask):
+    """More query tiles than the 512 resident workgroups: whole tiles first,
+    the leftover tiles' key blocks spread over every workgroup and merged by
+    the combine kernel (the running max, the rescaled sums)."""
+    print(f"[gpu] split attention B={B} T={T} S={S} H={H} d={d} mask={mask}", flush=True)
+    q = bf(normal("sq", (B, T, H * d), 2.0))
+    k = bf(normal("sk", (B, S, H * d)))
+    v = bf(normal("sv", (B, S, H * d)))
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    ins = [model.Placeholder([B, 1, n, H * d]) for n in (T, S, S)]
+    extra = []
+    if mask == "length":
+        kl = model.Placeholder([1, 1, 1, 1], DT.Int32)
+        out = Layers.Attend(*ins, H, kl, nd.MaskType.KeySequenceLength)
+        extra = [HostTensor.FromInt32(np.array([S - 37]), 1, 1, 1, 1)]
+        ref = oracle.mha(q, k, v, H, mask_kind=1, key_len=S - 37)
+    elif mask == "table":
+        table = (normal("tbl", (B, 1, T, S)) > -0.5).astype(np.int32)
+        tb = model.Placeholder([B, 1, T, S], DT.Int32)
+        out = Layers.Attend(*ins, H, Layers.Broadcast(tb, [B, H, T, S]), nd.MaskType.Boolean)
+        extra = [HostTensor.FromInt32(table)]
+        ref = oracle.mha(q, k, v, H, mask_kind=2, mask=table)
+    else:
+        out = Layers.Attend(*ins, H)
+        ref = oracle.mha(q, k, v, H)
+    model.Compile([out])
+    got = run(model, *[HostTensor.FromFloats(a.reshape(B, 1, -1, H * d)).ConvertTo(DT.BFloat16) for a in (q, k, v)],
+              *extra)[0]
+    err = rel_err(got.reshape(ref.shape), ref)
+    print(f"[gpu]   rel err {err:.2e}", flush=True)
+    assert err <= BF16_TOL
