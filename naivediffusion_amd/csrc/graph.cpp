@@ -1308,6 +1308,33 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     o = c.pack(o, sched);
   }
 
+  // Pair adjacent independent linears of equal N and K (the image and text
+  // streams' projections): they run as one launch, the second's row tiles
+  // after the first's (i5 = 1 on the first, 2 on the second).
+  for (size_t i = 0; i + 1 < sched.size(); i++) {
+    GNode& x = sched[i];
+    GNode& y = sched[i + 1];
+    if (x.op != OP_LINEAR || y.op != OP_LINEAR || x.i5 || y.i5) continue;
+    const GValue& wx = c.values[x.in[1]];
+    const GValue& wy = c.values[y.in[1]];
+    const GValue& ax = c.values[x.in[0]];
+    const GValue& ay = c.values[y.in[0]];
+    if (wx.quant || wy.quant || ax.dtype != ay.dtype || wx.dtype != wy.dtype) continue;
+    if (ax.dtype != NDX_BF16 && ax.dtype != NDX_F16) continue;
+    if (wx.v.size[2] != wy.v.size[2] || ax.v.size[3] != ay.v.size[3]) continue;
+    if (ax.v.size[0] * ax.v.size[1] != ay.v.size[0] * ay.v.size[1]) continue;
+    if (ax.v.size[2] <= 4 || ay.v.size[2] <= 4) continue;  // GEMVs stay single
+    if (!gemm_pair_pays(ax.v.size[2], ay.v.size[2], wx.v.size[2], ax.v.size[3], ax.v.size[0] * ax.v.size[1]))
+      continue;
+    bool dependent = false;
+    for (int id : y.in)
+      if (id >= 0 && c.values[id].base == c.values[x.out].base) dependent = true;
+    if (dependent) continue;
+    x.i5 = 1;
+    y.i5 = 2;
+    i++;
+  }
+
   auto* m = new ndx_model();
   try {
     m->dev = g->dev;
@@ -1324,6 +1351,11 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       m->out_slot[outs[k]] = (int)k;
     }
     for (auto& n : m->nodes) prof_info(n, m->values);
+    for (size_t i = 0; i + 1 < m->nodes.size(); i++)
+      if (m->nodes[i].op == OP_LINEAR && m->nodes[i].i5 == 1) {
+        m->nodes[i].flops += m->nodes[i + 1].flops;
+        m->nodes[i].bytes += m->nodes[i + 1].bytes;
+      }
     for (const auto* t : g->consts->tensors) m->persistent += t->bytes;
 
     // Lifetimes and the arena.
@@ -1364,11 +1396,16 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     };
     for (int i = 0; i < (int)m->nodes.size(); i++) {
       GNode& node = m->nodes[i];
-      int id = node.out;
       live.erase(std::remove_if(live.begin(), live.end(), [&](const Live& l) { return l.last < i; }), live.end());
-      if (m->out_slot[id] < 0)
-        m->arena_off[id] =
-            place(int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype), std::max(last[id], i));
+      // The second of a paired linear is written by the first's launch: its
+      // output is placed (and live) from there.
+      if (node.op == OP_LINEAR && node.i5 == 2) continue;
+      for (int k = 0; k < (node.op == OP_LINEAR && node.i5 == 1 ? 2 : 1); k++) {
+        const int id = m->nodes[i + k].out;
+        if (m->out_slot[id] < 0)
+          m->arena_off[id] =
+              place(int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype), std::max(last[id], i + k));
+      }
       if (node.scratch_bytes > 0) node.scratch_off = place(node.scratch_bytes, i);
     }
     m->arena_bytes = (size_t)top;
@@ -1412,6 +1449,62 @@ struct Runner {
   }
   const GValue& val(int id) { return m->values[id]; }
 
+  // The GEMM of a linear node (x [B,1,M,K] rows, W [N,K], epilogue inputs).
+  GemmArgs linear_args(const GNode& n) {
+    const GValue& x = val(n.in[0]);
+    const GValue& w = val(n.in[1]);
+    const GValue& o = val(n.out);
+    GemmArgs a{};
+    int64_t ld, bs;
+    rows_layout(x.v, ld, bs);
+    a.a = ptr(n.in[0]);
+    a.lda = ld;
+    a.batch_a = bs;
+    a.a_dtype = x.dtype;
+    a.M = (int)x.v.size[2];
+    a.K = (int)x.v.size[3];
+    a.batch = (int)(x.v.size[0] * x.v.size[1]);
+    a.N = (int)w.v.size[2];
+    if (w.quant) {
+      a.w = w.data->ptr;
+      a.ldw = w.v.size[3];
+      a.w_dtype = NDX_I8;
+      a.scales = w.scales->ptr;
+      a.qblock = w.qblock;
+      a.lds = w.v.size[3] / w.qblock;
+      a.s_dtype = w.scales->dtype;
+    } else {
+      a.w = ptr(n.in[1]);
+      a.ldw = w.v.size[2] > 1 ? w.v.stride[2] : w.v.size[3];
+      a.w_dtype = w.dtype;
+    }
+    a.batch_w = 0;
+    a.c = ptr(n.out);
+    a.ldc = a.N;
+    a.batch_c = int64_t(a.M) * a.N;
+    a.c_dtype = o.dtype;
+    if (n.in[2] >= 0) {
+      a.bias = ptr(n.in[2]);
+      a.bias_dtype = val(n.in[2]).dtype;
+    }
+    a.epilogue = n.i0;
+    if (n.in[3] >= 0) {
+      const GValue& gt = val(n.in[3]);
+      a.gate = ptr(n.in[3]);
+      a.gate_dtype = gt.dtype;
+      a.batch_gate = (gt.v.size[0] > 1) ? gt.v.stride[0] : (gt.v.size[1] > 1 ? gt.v.stride[1] : 0);
+    }
+    if (n.in[4] >= 0) {
+      const GValue& r = val(n.in[4]);
+      rows_layout(r.v, ld, bs);
+      a.resid = ptr(n.in[4]);
+      a.ldr = ld;
+      a.batch_r = bs;
+      a.r_dtype = r.dtype;
+    }
+    return a;
+  }
+
   void elem(int op, int a, int b, int o, float scale, float bias, hipStream_t s, const View4* out_view = nullptr,
             void* out_p = nullptr) {
     ElemArgs e{};
@@ -1450,58 +1543,17 @@ struct Runner {
         break;
       }
       case OP_LINEAR: {
-        const GValue& x = val(n.in[0]);
-        const GValue& w = val(n.in[1]);
-        const GValue& o = val(n.out);
-        GemmArgs a{};
-        int64_t ld, bs;
-        rows_layout(x.v, ld, bs);
-        a.a = ptr(n.in[0]);
-        a.lda = ld;
-        a.batch_a = bs;
-        a.a_dtype = x.dtype;
-        a.M = (int)x.v.size[2];
-        a.K = (int)x.v.size[3];
-        a.batch = (int)(x.v.size[0] * x.v.size[1]);
-        a.N = (int)w.v.size[2];
-        if (w.quant) {
-          a.w = w.data->ptr;
-          a.ldw = w.v.size[3];
-          a.w_dtype = NDX_I8;
-          a.scales = w.scales->ptr;
-          a.qblock = w.qblock;
-          a.lds = w.v.size[3] / w.qblock;
-          a.s_dtype = w.scales->dtype;
+        if (n.i5 == 2) break;  // launched with the node before it
+        const GemmArgs a = linear_args(n);
+        if (n.i5 == 1) {
+          const GemmArgs b = linear_args(*(&n + 1));
+          if (!launch_gemm_pair(a, b, s)) {
+            launch_gemm(a, s);
+            launch_gemm(b, s);
+          }
         } else {
-          a.w = ptr(n.in[1]);
-          a.ldw = w.v.size[2] > 1 ? w.v.stride[2] : w.v.size[3];
-          a.w_dtype = w.dtype;
+          launch_gemm(a, s);
         }
-        a.batch_w = 0;
-        a.c = ptr(n.out);
-        a.ldc = a.N;
-        a.batch_c = int64_t(a.M) * a.N;
-        a.c_dtype = o.dtype;
-        if (n.in[2] >= 0) {
-          a.bias = ptr(n.in[2]);
-          a.bias_dtype = val(n.in[2]).dtype;
-        }
-        a.epilogue = n.i0;
-        if (n.in[3] >= 0) {
-          const GValue& gt = val(n.in[3]);
-          a.gate = ptr(n.in[3]);
-          a.gate_dtype = gt.dtype;
-          a.batch_gate = (gt.v.size[0] > 1) ? gt.v.stride[0] : (gt.v.size[1] > 1 ? gt.v.stride[1] : 0);
-        }
-        if (n.in[4] >= 0) {
-          const GValue& r = val(n.in[4]);
-          rows_layout(r.v, ld, bs);
-          a.resid = ptr(n.in[4]);
-          a.ldr = ld;
-          a.batch_r = bs;
-          a.r_dtype = r.dtype;
-        }
-        launch_gemm(a, s);
         break;
       }
       case OP_GEMM: {
@@ -1793,16 +1845,20 @@ void run_nodes(ndx_model* m, Runner& r) {
     const GNode& n = m->nodes[i];
     std::string fam = n.family;
     if (n.op == OP_LINEAR) {
-      GemmArgs probe{};
-      const GValue& x = m->values[n.in[0]];
-      const GValue& w = m->values[n.in[1]];
-      probe.a_dtype = x.dtype;
-      probe.w_dtype = w.quant ? NDX_I8 : w.dtype;
-      probe.M = (int)(x.v.size[2]);
-      probe.N = (int)w.v.size[2];
-      probe.K = (int)x.v.size[3];
-      probe.batch = (int)(x.v.size[0] * x.v.size[1]);
-      fam = gemm_family(probe);
+      if (n.i5 == 2) continue;  // timed with the node before it
+      auto probe = [&](const GNode& k) {
+        GemmArgs p{};
+        const GValue& x = m->values[k.in[0]];
+        const GValue& w = m->values[k.in[1]];
+        p.a_dtype = x.dtype;
+        p.w_dtype = w.quant ? NDX_I8 : w.dtype;
+        p.M = (int)(x.v.size[2]);
+        p.N = (int)w.v.size[2];
+        p.K = (int)x.v.size[3];
+        p.batch = (int)(x.v.size[0] * x.v.size[1]);
+        return p;
+      };
+      fam = n.i5 == 1 ? gemm_pair_family(probe(n), probe(m->nodes[i + 1])) : gemm_family(probe(n));
     }
     ProfEntry& e = m->prof[fam];
     e.launches++;

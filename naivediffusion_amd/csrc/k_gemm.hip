@@ -360,8 +360,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 // the MFMAs of step s run.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// a0 and a1 are two products with the same N, K and batch run as one grid
+// (a0's row tiles first, then a1's); a1.M = 0 for a single product.
 template <int BM, int BN, int WM, int WN, typename T, bool CONV>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a, int grid) {
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
+                                                                                    int grid) {
   typedef typename MfmaOp<T>::V V;
   constexpr int WAVES_N = BN / WN;
   constexpr int NW = (BM / WM) * (BN / WN);
@@ -376,7 +379,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   T (*Bs)[BN * BK] = reinterpret_cast<T (*)[BN * BK]>(smem + 2 * BM * BK * sizeof(T));
 
   int tm, tn;
-  if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
+  const int tiles_m0 = (a0.M + BM - 1) / BM;
+  if (!tile_of(blockIdx.x, grid, tiles_m0 + (a1.M + BM - 1) / BM, (a0.N + BN - 1) / BN, tm, tn)) return;
+  const bool second = tm >= tiles_m0;
+  const GemmArgs& a = second ? a1 : a0;
+  if (second) tm -= tiles_m0;
   const int64_t bidx = blockIdx.y;
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -775,7 +782,7 @@ static bool spans_fit(const GemmArgs& a) {
 // DiTs' and the UNet's GEMM shapes on MI355X (rows 154 to 13778, N 640 to
 // 12288, K 640 to 12288): within 0.2% of the best tile on average, 3.5% at
 // worst. Index 0..3: 256x256, 128x128, 64x128, 64x64.
-static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
+static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch, double* model_time = nullptr) {
   struct Tile { int bm, bn, per_cu; double rate; double k0; };
   static const Tile tiles[4] = {
       {256, 256, 1, 1000.0, 512.0}, {128, 128, 2, 920.0, 128.0}, {64, 128, 3, 700.0, 128.0}, {64, 64, 4, 560.0, 128.0}};
@@ -792,6 +799,8 @@ static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch) {
       best_t = time;
     }
   }
+  // In microseconds: 2 flops per multiply-add over rates in TFLOP/s.
+  if (model_time) *model_time = best_t * 2.0 * 1e-6;
   return best;
 }
 
@@ -881,14 +890,16 @@ static void launch_mfma(const GemmArgs& a, hipStream_t s) {
 }
 
 template <int BM, int BN, int WM, int WN, bool CONV = false>
-static void launch_mfma_lds(const GemmArgs& a, hipStream_t s) {
-  int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* second = nullptr) {
+  GemmArgs a1{};
+  if (second) a1 = *second;
+  int tiles = ((a.M + BM - 1) / BM + (a1.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   int grid = (tiles + 7) / 8 * 8;
   dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
   if (a.a_dtype == NDX_BF16)
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, CONV>), g, b, 0, s, a, grid);
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, CONV>), g, b, 0, s, a, a1, grid);
   else
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, CONV>), g, b, 0, s, a, grid);
+    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, CONV>), g, b, 0, s, a, a1, grid);
 }
 
 // ---- implicit-GEMM convolution ----------------------------------------------
@@ -951,6 +962,42 @@ void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
     case CK_64x128: launch_mfma_lds<64, 128, 32, 64, true>(g, s); break;
     default: launch_mfma_lds<64, 64, 32, 32, true>(g, s); break;
   }
+}
+
+static bool is_lds_kind(GemmKind k) {
+  return k == K_LDS_256 || k == K_LDS_128 || k == K_LDS_64x128 || k == K_LDS_64x64;
+}
+
+bool gemm_pair_pays(int64_t M1, int64_t M2, int64_t N, int64_t K, int64_t batch) {
+  // One launch must beat two by the model (a pair can push the tile count
+  // past a round of the machine's slots), counting 5 us fixed per launch.
+  double t1, t2, t12;
+  pick_tile(M1, N, K, batch, &t1);
+  pick_tile(M2, N, K, batch, &t2);
+  pick_tile(M1 + M2, N, K, batch, &t12);
+  return t12 + 5.0 < t1 + t2 + 10.0;
+}
+
+bool launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t s) {
+  if (a.M == 0 || b.M == 0 || a.N != b.N || a.K != b.K || a.batch != b.batch || a.a_dtype != b.a_dtype ||
+      a.w_dtype != b.w_dtype || !is_lds_kind(choose(a)) || !is_lds_kind(choose(b)))
+    return false;
+  GemmArgs both = a;
+  both.M = a.M + b.M;
+  switch (choose(both)) {
+    case K_LDS_256: launch_mfma_lds<256, 256, 128, 128>(a, s, &b); break;
+    case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s, &b); break;
+    case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s, &b); break;
+    case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s, &b); break;
+    default: return false;
+  }
+  return true;
+}
+
+const char* gemm_pair_family(const GemmArgs& a, const GemmArgs& b) {
+  GemmArgs both = a;
+  both.M = a.M + b.M;
+  return gemm_family(both);
 }
 
 void launch_gemm(const GemmArgs& a, hipStream_t s) {

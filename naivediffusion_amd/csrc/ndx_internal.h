@@ -219,5 +219,12 @@ void quantize_host(const void* w, int dtype, int64_t rows, int64_t cols, int blo
 
 // Which GEMM kernel a shape goes to, and the algorithmic work, for profiling.
 const char* gemm_family(const GemmArgs& a);
+// Two independent products with equal N, K, batch and types as one launch
+// (the second's row tiles after the first's); false when they cannot share
+// a kernel, and then nothing was launched.
+bool launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t s);
+// Whether one launch of the two products is modelled faster than two.
+bool gemm_pair_pays(int64_t M1, int64_t M2, int64_t N, int64_t K, int64_t batch);
+const char* gemm_pair_family(const GemmArgs& a, const GemmArgs& b);
 
 }  // namespace ndx

@@ -201,8 +201,11 @@ def build_block(model: ModelBuilder, W: _W, i: int, cfg: MmditConfig, x_img, x_t
         mod[s] = Layers.Linear(model, silu_temb, W(f"{p[s]}_mod.weight"), W(f"{p[s]}_mod.bias", "wide"))
     for s in STREAMS:
         h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 0, D), _chunk(mod[s], 1, D), eps, compute)
+    # The two streams' projections are emitted back to back: the compiler
+    # runs each such pair as one launch.
+    qkvs = {s: Layers.Linear(model, h[s], W(f"{p[s]}_qkv.weight"), W(f"{p[s]}_qkv.bias", "bias")) for s in STREAMS}
     for s in STREAMS:
-        qkv = Layers.Linear(model, h[s], W(f"{p[s]}_qkv.weight"), W(f"{p[s]}_qkv.bias", "bias"))
+        qkv = qkvs[s]
         r0, nr = rows[s]
         c = Ops.Slice(cos, [0, r0, 0, 0], [1, nr, 1, 64])
         sn = Ops.Slice(sin, [0, r0, 0, 0], [1, nr, 1, 64])
@@ -224,10 +227,10 @@ def build_block(model: ModelBuilder, W: _W, i: int, cfg: MmditConfig, x_img, x_t
                              gate=_chunk(mod[s], 2, D), residual=x[s])
     for s in STREAMS:
         h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 3, D), _chunk(mod[s], 4, D), eps, compute)
+    f = {s: Layers.Linear(model, h[s], W(f"{p[s]}_fc1.weight"), W(f"{p[s]}_fc1.bias", "bias"),
+                          activation="gelu_tanh") for s in STREAMS}
     for s in STREAMS:
-        f = Layers.Linear(model, h[s], W(f"{p[s]}_fc1.weight"), W(f"{p[s]}_fc1.bias", "bias"),
-                          activation="gelu_tanh")
-        x[s] = Layers.Linear(model, f, W(f"{p[s]}_fc2.weight"), W(f"{p[s]}_fc2.bias", "bias"),
+        x[s] = Layers.Linear(model, f[s], W(f"{p[s]}_fc2.weight"), W(f"{p[s]}_fc2.bias", "bias"),
                              gate=_chunk(mod[s], 5, D), residual=x[s])
     return x["img"], x["txt"]
 

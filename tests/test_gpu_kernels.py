@@ -540,3 +540,37 @@ def test_attention_split_schedule(device, B, T, S, H, d, mask):
     err = rel_err(got.reshape(ref.shape), ref)
     print(f"[gpu]   rel err {err:.2e}", flush=True)
     assert err <= BF16_TOL
+
+
+@pytest.mark.parametrize("M1,M2,K,N", [(1000, 77, 512, 384), (5376 // 4, 256, 1024, 1536), (300, 300, 256, 2056)])
+def test_paired_linears_run_as_one_launch(device, M1, M2, K, N):
+    """Two independent linears of equal N and K emitted back to back (the
+    image and text streams' projections) run as one launch, each with its
+    own epilogue; a third that reads the first's output is not paired."""
+    print(f"[gpu] paired linears M1={M1} M2={M2} K={K} N={N}", flush=True)
+    x1, x2 = bf(normal("px1", (1, 1, M1, K))), bf(normal("px2", (1, 1, M2, K)))
+    w1, w2 = bf(normal("pw1", (N, K), 0.05)), bf(normal("pw2", (N, K), 0.05))
+    b1, b2 = bf(normal("pb1", (N,), 0.05)), bf(normal("pb2", (N,), 0.05))
+    r2 = normal("pr2", (1, 1, M2, N))
+    g2 = normal("pg2", (1, 1, 1, N))
+    w3 = bf(normal("pw3", (N, N), 0.05))
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    p1 = model.Placeholder([1, 1, M1, K])
+    p2 = model.Placeholder([1, 1, M2, K])
+    pr = model.Placeholder([1, 1, M2, N], DT.Float32)
+    pg = model.Placeholder([1, 1, 1, N], DT.Float32)
+    y1 = Layers.Linear(model, p1, HostTensor.FromFloats(w1), HostTensor.FromFloats(b1), activation="gelu_tanh")
+    y2 = Layers.Linear(model, p2, HostTensor.FromFloats(w2), HostTensor.FromFloats(b2), gate=pg, residual=pr)
+    y3 = Layers.Linear(model, y1, HostTensor.FromFloats(w3))
+    model.Compile([y1, y2, y3])
+    model.Compiled.SetProfiling(True)
+    o1, o2, o3 = run(model, HostTensor.FromFloats(x1).ConvertTo(DT.BFloat16),
+                     HostTensor.FromFloats(x2).ConvertTo(DT.BFloat16), HostTensor.FromFloats(r2), HostTensor.FromFloats(g2))
+    launches = sum(e["launches"] for k, e in model.Compiled.Profile().items() if k.startswith("gemm"))
+    assert launches == 2, model.Compiled.Profile()
+    e1 = oracle.gelu_tanh(oracle.linear(x1, w1, b1))
+    e2 = r2 + g2 * bf(oracle.linear(x2, w2, b2))
+    e3 = oracle.linear(bf(e1), w3)
+    assert rel_err(o1, e1) <= BF16_TOL
+    assert rel_err(o2 - r2, e2 - r2) <= BF16_TOL
+    assert rel_err(o3, e3) <= BF16_TOL
