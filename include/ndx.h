@@ -138,6 +138,13 @@ NDX_API ndx_status ndx_quantize_block_int8_device(ndx_tensor* w, int32_t block,
 NDX_API ndx_status ndx_graph_create(ndx_device* device, int32_t dtype, int32_t int8_weights,
                                     ndx_graph** out);
 NDX_API ndx_status ndx_graph_destroy(ndx_graph* graph);
+/* No counterpart in the reference (DirectML schedules a graph itself): the
+ * stream that operations emitted from now on run on, 0 (the device's, the
+ * default) or 1 (a second stream of the same default priority). Independent
+ * chains on the two streams run concurrently; the compiled model waits
+ * across streams where one reads what the other wrote or reuses its memory,
+ * and a run ends with both streams joined on the device stream. */
+NDX_API ndx_status ndx_graph_set_stream(ndx_graph* graph, int32_t stream);
 /* ModelBuilder.Placeholder, Graph/ModelBuilder.cs:93-98 (DmlGraph.Input,
  * owned false): bound by position at run time. */
 NDX_API ndx_status ndx_graph_input(ndx_graph* graph, int32_t dtype, const int64_t* shape,

@@ -79,6 +79,7 @@ SIGNATURES = [
     ("ndx_quantize_block_int8_device", i32, [vp, i32, i32, vp, vp]),
     ("ndx_graph_create", i32, [vp, i32, i32, P(vp)]),
     ("ndx_graph_destroy", i32, [vp]),
+    ("ndx_graph_set_stream", i32, [vp, i32]),
     ("ndx_graph_input", i32, [vp, i32, P(i64), i32, P(i32)]),
     ("ndx_graph_constant", i32, [vp, i32, P(i64), i32, vp, i32, P(i32)]),
     ("ndx_graph_constant_device", i32, [vp, vp, P(i32)]),

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <functional>
+#include <array>
 #include <map>
 #include <memory>
 #include <sstream>
@@ -68,6 +69,8 @@ struct GNode {
   int seg[3][2] = {{-1, -1}, {-1, -1}, {-1, -1}};
   // scratch in the arena, live only while this node runs
   int64_t scratch_bytes = 0, scratch_off = -1;
+  // the stream (0 the device's, 1 the second) the node runs on
+  int lane = 0;
   // profiling
   std::string family;
   double flops = 0, bytes = 0;
@@ -151,7 +154,9 @@ struct ndx_graph {
     values[id].base = id;
     return id;
   }
+  int lane = 0;  // ndx_graph_set_stream: the lane new nodes go to
   int emit(GNode n, int dtype, const int64_t* size4, int rank) {
+    n.lane = lane;
     n.out = node_output(dtype, size4, rank);
     values[n.out].producer = (int)nodes.size();
     nodes.push_back(n);
@@ -179,6 +184,12 @@ struct ndx_model {
   int kernels = 0;
   bool profiling = false;
   std::vector<hipEvent_t> events;
+  // Two lanes: per node, the latest node of each lane it must wait for (-1
+  // none), the event a node records for others (-1 none), and the events.
+  bool two_lanes = false;
+  std::vector<std::array<int, 2>> waits;
+  std::vector<int> signal;
+  std::vector<hipEvent_t> lane_events;  // [signals..., start join, end join]
   std::map<std::string, ProfEntry> prof;
 };
 
@@ -261,6 +272,14 @@ NDX_API ndx_status ndx_graph_create(ndx_device* device, int32_t dtype, int32_t i
 NDX_API ndx_status ndx_graph_destroy(ndx_graph* graph) {
   NDX_TRY
   delete graph;
+  NDX_CATCH
+}
+
+NDX_API ndx_status ndx_graph_set_stream(ndx_graph* g, int32_t stream) {
+  NDX_TRY
+  NEED(g);
+  if (stream != 0 && stream != 1) fail(NDX_INVALID_ARG, "the stream is 0 or 1");
+  g->lane = stream;
   NDX_CATCH
 }
 
@@ -1003,6 +1022,7 @@ struct Compiler {
   ndx_graph* g;
   std::vector<GValue> values;
   std::vector<GNode> nodes;
+  int lane = 0;  // of the node being scheduled: the nodes inserted for it share it
 
   int new_owner(int dtype, const View4& shape_from, int rank) {
     GValue v;
@@ -1055,6 +1075,7 @@ struct Compiler {
     n.i0 = ELEM_COPY;
     n.f0 = 1.f;
     n.out = out;
+    n.lane = lane;
     sched.push_back(n);
     return out;
   }
@@ -1134,6 +1155,77 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
 
 }  // namespace
 
+// The cross-lane waits of a two-lane model: a node waits for the latest
+// node of the other lane that produced a value it reads, and, where the
+// arena hands it bytes that a dead value occupied, for every node of the
+// other lane that touched that value. A paired linear's second half runs
+// inside the first's launch and counts as it.
+static void plan_lanes(ndx_model* m, const std::vector<int>& last) {
+  const int nn = (int)m->nodes.size(), nv = (int)m->values.size();
+  m->two_lanes = false;
+  for (const auto& n : m->nodes)
+    if (n.lane) m->two_lanes = true;
+  if (!m->two_lanes) return;
+  auto exec = [&](int j) { return (m->nodes[j].op == OP_LINEAR && m->nodes[j].i5 == 2) ? j - 1 : j; };
+  std::vector<int> prod(nv, -1);
+  for (int i = 0; i < nn; i++) prod[m->nodes[i].out] = exec(i);
+  m->waits.assign(nn, {-1, -1});
+  auto dep = [&](int i, int j) {
+    if (j < 0) return;
+    i = exec(i);
+    j = exec(j);
+    const int lj = m->nodes[j].lane;
+    if (m->nodes[i].lane == lj || j >= i) return;
+    m->waits[i][lj] = std::max(m->waits[i][lj], j);
+  };
+  std::vector<std::vector<int>> users(nv);
+  for (int i = 0; i < nn; i++) {
+    const GNode& n = m->nodes[i];
+    auto use = [&](int id) {
+      if (id < 0) return;
+      const int b = m->values[id].base;
+      dep(i, prod[b]);
+      users[b].push_back(exec(i));
+    };
+    for (int id : n.in) use(id);
+    if (n.op == OP_ATTN)
+      for (int j = 0; j < 3; j++) {
+        use(n.seg[j][0]);
+        use(n.seg[j][1]);
+      }
+    users[n.out].push_back(exec(i));
+  }
+  struct Alloc {
+    int64_t off, size;
+    int first, last, base;
+  };
+  std::vector<Alloc> al;
+  for (int id = 0; id < nv; id++) {
+    if (m->arena_off[id] < 0 || m->values[id].base != id || prod[id] < 0) continue;
+    const int64_t bytes = (int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype) + 255) & ~int64_t(255);
+    al.push_back({m->arena_off[id], bytes, prod[id], exec(std::max(last[id], prod[id])), id});
+  }
+  for (int i = 0; i < nn; i++)
+    if (m->nodes[i].scratch_bytes > 0)
+      al.push_back({m->nodes[i].scratch_off, (m->nodes[i].scratch_bytes + 255) & ~int64_t(255), exec(i), exec(i), -1 - i});
+  for (const Alloc& a : al)
+    for (const Alloc& b : al) {
+      if (b.last >= a.first || a.off >= b.off + b.size || b.off >= a.off + a.size) continue;
+      if (b.base >= 0) {
+        for (int u : users[b.base]) dep(a.first, u);
+      } else {
+        dep(a.first, -1 - b.base);
+      }
+    }
+  m->signal.assign(nn, -1);
+  int ne = 0;
+  for (int i = 0; i < nn; i++)
+    for (int t = 0; t < 2; t++)
+      if (m->waits[i][t] >= 0 && m->signal[m->waits[i][t]] < 0) m->signal[m->waits[i][t]] = ne++;
+  m->lane_events.resize(ne + 2);
+  for (auto& e : m->lane_events) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+}
+
 extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* outputs, int32_t count,
                                                 ndx_model** out) {
   NDX_TRY
@@ -1211,6 +1303,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
   for (size_t i = 0; i < src.size(); i++) {
     if (!need_node[i]) continue;
     GNode n = src[i];
+    c.lane = n.lane;
     auto rows_ok = [&](int id) {
       int64_t ld, bs;
       return id < 0 || rows_layout(c.values[id].v, ld, bs);
@@ -1286,6 +1379,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
             conv_gemm_eligible(x.dtype, w.dtype, (int)x.v.size[1])) {
           GNode t;
           t.op = OP_NHWC;
+          t.lane = n.lane;
           t.in = {n.in[0]};
           t.out = c.new_owner(x.dtype, x.v, 4);
           sched.push_back(t);
@@ -1301,6 +1395,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     sched.push_back(n);
   }
 
+  c.lane = 0;
   // Outputs must be packed owners: copy a view out.
   for (auto& o : outs) {
     const GValue& v = c.values[o];
@@ -1314,7 +1409,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
   for (size_t i = 0; i + 1 < sched.size(); i++) {
     GNode& x = sched[i];
     GNode& y = sched[i + 1];
-    if (x.op != OP_LINEAR || y.op != OP_LINEAR || x.i5 || y.i5) continue;
+    if (x.op != OP_LINEAR || y.op != OP_LINEAR || x.i5 || y.i5 || x.lane != y.lane) continue;
     const GValue& wx = c.values[x.in[1]];
     const GValue& wy = c.values[y.in[1]];
     const GValue& ax = c.values[x.in[0]];
@@ -1413,6 +1508,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       m->arena_alloc = pool_round(m->arena_bytes);
       m->arena = m->dev->alloc(m->arena_alloc);
     }
+    plan_lanes(m, last);
     for (auto& n : m->nodes) m->kernels += (n.op == OP_JOIN) ? (int)n.in.size() : 1;
   } catch (...) {
     delete m;
@@ -1821,21 +1917,40 @@ void check_inputs(ndx_model* m, ndx_tensor* const* inputs, int32_t n_inputs) {
 
 void run_nodes(ndx_model* m, Runner& r) {
   hipStream_t s = m->dev->stream;
-  if (!m->profiling) {
-    for (const auto& n : m->nodes) r.launch(n, s);
-    hip_check(hipGetLastError(), "kernel launch");
-    return;
+  hipStream_t st[2] = {s, m->two_lanes ? m->dev->aux_stream() : s};
+  const int ne = (int)m->lane_events.size();
+  if (m->two_lanes) {
+    // The second lane starts after what the device stream holds (inputs,
+    // the previous run) and the device stream ends after the second lane.
+    hip_check(hipEventRecord(m->lane_events[ne - 2], s), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(st[1], m->lane_events[ne - 2], 0), "hipStreamWaitEvent");
   }
   size_t need = m->nodes.size() * 2;
-  while (m->events.size() < need) {
+  while (m->profiling && m->events.size() < need) {
     hipEvent_t e;
     hip_check(hipEventCreate(&e), "hipEventCreate");
     m->events.push_back(e);
   }
   for (size_t i = 0; i < m->nodes.size(); i++) {
-    hip_check(hipEventRecord(m->events[2 * i], s), "hipEventRecord");
-    r.launch(m->nodes[i], s);
-    hip_check(hipEventRecord(m->events[2 * i + 1], s), "hipEventRecord");
+    const GNode& n = m->nodes[i];
+    hipStream_t ns = st[n.lane & 1];
+    if (m->two_lanes)
+      for (int t = 0; t < 2; t++)
+        if (m->waits[i][t] >= 0)
+          hip_check(hipStreamWaitEvent(ns, m->lane_events[m->signal[m->waits[i][t]]], 0), "hipStreamWaitEvent");
+    if (m->profiling) hip_check(hipEventRecord(m->events[2 * i], ns), "hipEventRecord");
+    r.launch(n, ns);
+    if (m->profiling) hip_check(hipEventRecord(m->events[2 * i + 1], ns), "hipEventRecord");
+    if (m->two_lanes && m->signal[i] >= 0)
+      hip_check(hipEventRecord(m->lane_events[m->signal[i]], ns), "hipEventRecord");
+  }
+  if (m->two_lanes) {
+    hip_check(hipEventRecord(m->lane_events[ne - 1], st[1]), "hipEventRecord");
+    hip_check(hipStreamWaitEvent(s, m->lane_events[ne - 1], 0), "hipStreamWaitEvent");
+  }
+  if (!m->profiling) {
+    hip_check(hipGetLastError(), "kernel launch");
+    return;
   }
   hip_check(hipGetLastError(), "kernel launch");
   hip_check(hipStreamSynchronize(s), "profiled run");
@@ -1983,7 +2098,9 @@ NDX_API ndx_status ndx_model_release(ndx_model* m) {
     (void)hipStreamSynchronize(m->dev->stream);
     m->dev->release(m->arena, m->arena_alloc);
   }
+  if (m->two_lanes && m->dev->aux) (void)hipStreamSynchronize(m->dev->aux);
   for (auto e : m->events) (void)hipEventDestroy(e);
+  for (auto e : m->lane_events) (void)hipEventDestroy(e);
   delete m;
   NDX_CATCH
 }

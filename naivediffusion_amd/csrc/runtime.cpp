@@ -151,6 +151,15 @@ using namespace ndx;
 
 // ---- device -------------------------------------------------------------------
 
+hipStream_t ndx_device::aux_stream() {
+  if (!aux) {
+    // Default priority, like the device stream (streams of different
+    // priorities are never mixed here).
+    hip_check(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking), "hipStreamCreate");
+  }
+  return aux;
+}
+
 void* ndx_device::alloc(size_t bytes) {
   check_usable();
   if (fault == 1) {
@@ -279,9 +288,12 @@ NDX_API ndx_status ndx_device_destroy(ndx_device* device) {
   NDX_TRY
   if (!device || device->destroyed) return NDX_OK;
   (void)hipStreamSynchronize(device->stream);
+  if (device->aux) (void)hipStreamSynchronize(device->aux);
   device->trim();
   (void)hipStreamDestroy(device->stream);
   device->stream = nullptr;
+  if (device->aux) (void)hipStreamDestroy(device->aux);
+  device->aux = nullptr;
   device->destroyed = true;
   // Tensors and models still alive keep the object until they go.
   if (device->refs == 0) delete device;

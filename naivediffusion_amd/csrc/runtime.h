@@ -11,6 +11,7 @@
 struct ndx_device {
   int id = 0;
   hipStream_t stream = nullptr;
+  hipStream_t aux = nullptr;  // the second lane of a compiled model, made on first use
   std::string name;
   bool lost = false;
   bool destroyed = false;  // ndx_device_destroy ran; freed when refs drops to 0
@@ -24,6 +25,7 @@ struct ndx_device {
   size_t live_bytes = 0;
 
   void* alloc(size_t bytes);
+  hipStream_t aux_stream();
   // Returns a block to the pool; after destroy it is freed instead, and the
   // device object goes when the last block does.
   void release(void* p, size_t bytes);

@@ -9,6 +9,7 @@ Every operator runs in libndx.so on the GPU.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Optional, Sequence
 
@@ -58,6 +59,19 @@ class Graph:
 
     def Input(self, dataType: HostDataType, sizes: Sequence[int]) -> "Expression":
         return self._new("ndx_graph_input", int(dataType), _lib.shape_array(sizes), len(sizes))
+
+    def SetStream(self, stream: int) -> None:
+        """The stream (0 or 1) operations emitted from now on run on."""
+        call("ndx_graph_set_stream", self._h, int(stream))
+
+    @contextlib.contextmanager
+    def Stream(self, stream: int):
+        """with graph.Stream(1): ... emits onto the second stream, then back to 0."""
+        self.SetStream(stream)
+        try:
+            yield self
+        finally:
+            self.SetStream(0)
 
     def Dispose(self):
         if self._h is not None:

@@ -184,36 +184,39 @@ def _chunk(mod, i: int, D: int):
 
 
 def build_block(model: ModelBuilder, W: _W, i: int, cfg: MmditConfig, x_img, x_txt, silu_temb, cos, sin,
-                compute: HostDataType, key_len=None):
+                compute: HostDataType, key_len=None, two_streams: bool = True):
     """One dual-stream joint block. x_img [B, 1, Ni, D] and x_txt [B, 1, Nt,
     D] are the fp32 residual streams; silu_temb [B, 1, 1, T]; cos/sin [1, N,
-    1, 64]. Returns the updated (x_img, x_txt)."""
+    1, 64]. Returns the updated (x_img, x_txt). With two_streams the text
+    stream's operations run on the second stream, beside the image stream's
+    (they meet at the joint attention)."""
     D, H, eps = cfg.width, cfg.heads, cfg.eps
     B, _, n_img, _ = x_img.Shape
     n_txt = x_txt.Shape[2]
     x = {"img": x_img, "txt": x_txt}
     rows = {"img": (0, n_img), "txt": (n_img, n_txt)}
     p = {s: f"blocks.{i}.{s}" for s in STREAMS}
+    g = model.Graph
+
+    def lane(s):
+        return g.Stream(1 if (two_streams and s == "txt") else 0)
+
     mod, h, q, k, v = {}, {}, {}, {}, {}
     for s in STREAMS:
-        # (shift1, scale1, gate1, shift2, scale2, gate2), fp32 like the
-        # reference's time path.
-        mod[s] = Layers.Linear(model, silu_temb, W(f"{p[s]}_mod.weight"), W(f"{p[s]}_mod.bias", "wide"))
-    for s in STREAMS:
-        h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 0, D), _chunk(mod[s], 1, D), eps, compute)
-    # The two streams' projections are emitted back to back: the compiler
-    # runs each such pair as one launch.
-    qkvs = {s: Layers.Linear(model, h[s], W(f"{p[s]}_qkv.weight"), W(f"{p[s]}_qkv.bias", "bias")) for s in STREAMS}
-    for s in STREAMS:
-        qkv = qkvs[s]
-        r0, nr = rows[s]
-        c = Ops.Slice(cos, [0, r0, 0, 0], [1, nr, 1, 64])
-        sn = Ops.Slice(sin, [0, r0, 0, 0], [1, nr, 1, 64])
-        q[s] = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, 0], [B, 1, nr, D]),
-                                          W(f"{p[s]}_norm_q.weight", "bias"), H, eps, c, sn, compute)
-        k[s] = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, D], [B, 1, nr, D]),
-                                          W(f"{p[s]}_norm_k.weight", "bias"), H, eps, c, sn, compute)
-        v[s] = Ops.Slice(qkv, [0, 0, 0, 2 * D], [B, 1, nr, D])
+        with lane(s):
+            # (shift1, scale1, gate1, shift2, scale2, gate2), fp32 like the
+            # reference's time path.
+            mod[s] = Layers.Linear(model, silu_temb, W(f"{p[s]}_mod.weight"), W(f"{p[s]}_mod.bias", "wide"))
+            h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 0, D), _chunk(mod[s], 1, D), eps, compute)
+            qkv = Layers.Linear(model, h[s], W(f"{p[s]}_qkv.weight"), W(f"{p[s]}_qkv.bias", "bias"))
+            r0, nr = rows[s]
+            c = Ops.Slice(cos, [0, r0, 0, 0], [1, nr, 1, 64])
+            sn = Ops.Slice(sin, [0, r0, 0, 0], [1, nr, 1, 64])
+            q[s] = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, 0], [B, 1, nr, D]),
+                                              W(f"{p[s]}_norm_q.weight", "bias"), H, eps, c, sn, compute)
+            k[s] = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, D], [B, 1, nr, D]),
+                                              W(f"{p[s]}_norm_k.weight", "bias"), H, eps, c, sn, compute)
+            v[s] = Ops.Slice(qkv, [0, 0, 0, 2 * D], [B, 1, nr, D])
     joint = [Ops.Join([t["img"], t["txt"]], 2) for t in (q, k, v)]
     if key_len is None:
         a = Layers.Attend(*joint, H)
@@ -221,22 +224,22 @@ def build_block(model: ModelBuilder, W: _W, i: int, cfg: MmditConfig, x_img, x_t
         from .graph import MaskType
         a = Layers.Attend(*joint, H, key_len, MaskType.KeySequenceLength)
     for s in STREAMS:
-        r0, nr = rows[s]
-        a_s = Ops.Slice(a, [0, 0, r0, 0], [B, 1, nr, D])
-        x[s] = Layers.Linear(model, a_s, W(f"{p[s]}_out.weight"), W(f"{p[s]}_out.bias", "bias"),
-                             gate=_chunk(mod[s], 2, D), residual=x[s])
-    for s in STREAMS:
-        h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 3, D), _chunk(mod[s], 4, D), eps, compute)
-    f = {s: Layers.Linear(model, h[s], W(f"{p[s]}_fc1.weight"), W(f"{p[s]}_fc1.bias", "bias"),
-                          activation="gelu_tanh") for s in STREAMS}
-    for s in STREAMS:
-        x[s] = Layers.Linear(model, f[s], W(f"{p[s]}_fc2.weight"), W(f"{p[s]}_fc2.bias", "bias"),
-                             gate=_chunk(mod[s], 5, D), residual=x[s])
+        with lane(s):
+            r0, nr = rows[s]
+            a_s = Ops.Slice(a, [0, 0, r0, 0], [B, 1, nr, D])
+            x[s] = Layers.Linear(model, a_s, W(f"{p[s]}_out.weight"), W(f"{p[s]}_out.bias", "bias"),
+                                 gate=_chunk(mod[s], 2, D), residual=x[s])
+            h[s] = Transformer.Modulate(x[s], _chunk(mod[s], 3, D), _chunk(mod[s], 4, D), eps, compute)
+            f = Layers.Linear(model, h[s], W(f"{p[s]}_fc1.weight"), W(f"{p[s]}_fc1.bias", "bias"),
+                              activation="gelu_tanh")
+            x[s] = Layers.Linear(model, f, W(f"{p[s]}_fc2.weight"), W(f"{p[s]}_fc2.bias", "bias"),
+                                 gate=_chunk(mod[s], 5, D), residual=x[s])
     return x["img"], x["txt"]
 
 
 def build_block_model(device: Device, cfg: MmditConfig, weights: dict, batch: int, n_img: int, n_txt: int,
-                      compute: HostDataType, int8: bool = False, block: int = 0, key_len: bool = False):
+                      compute: HostDataType, int8: bool = False, block: int = 0, key_len: bool = False,
+                      two_streams: bool = True):
     """A compiled single-block model. Inputs in order: x_img [B,1,Ni,D],
     x_txt [B,1,Nt,D], temb [B,1,1,D] (the time embedding before SiLU), cos,
     sin [1,N,1,64] (and the key length [1,1,1,1] when key_len). Outputs the
@@ -250,12 +253,12 @@ def build_block_model(device: Device, cfg: MmditConfig, weights: dict, batch: in
     cos = model.Placeholder([1, n_img + n_txt, 1, 64], HostDataType.Float32)
     sin = model.Placeholder([1, n_img + n_txt, 1, 64], HostDataType.Float32)
     kl = model.Placeholder([1, 1, 1, 1], HostDataType.Int32) if key_len else None
-    yi, yt = build_block(model, W, block, cfg, xi, xt, Layers.Silu(temb), cos, sin, compute, kl)
+    yi, yt = build_block(model, W, block, cfg, xi, xt, Layers.Silu(temb), cos, sin, compute, kl, two_streams)
     return model.Compile([yi, yt])
 
 
 def build_step_model(device: Device, cfg: MmditConfig, weights: dict, batch: int, n_txt: int, latent_h: int,
-                     latent_w: int, compute: HostDataType, int8: bool = False):
+                     latent_w: int, compute: HostDataType, int8: bool = False, two_streams: bool = True):
     """The full denoiser step as one compiled model (every GraphChain cut of
     the reference is a no-op here: everything is resident). Inputs: latent
     [B, C, H, W] fp32, text [B, 1, Nt, text_dim] fp32, the time sinusoid
@@ -280,7 +283,8 @@ def build_step_model(device: Device, cfg: MmditConfig, weights: dict, batch: int
                          W("time.linear_2.weight"), W("time.linear_2.bias", "wide"))
     silu_temb = Layers.Silu(temb)
     for i in range(cfg.blocks):
-        x_img, x_txt = build_block(model, W, i, cfg, x_img, x_txt, silu_temb, cos, sin, compute)
+        x_img, x_txt = build_block(model, W, i, cfg, x_img, x_txt, silu_temb, cos, sin, compute,
+                                   two_streams=two_streams)
     # Final layer: modulated LayerNorm (scale, shift) then the projection,
     # wide (QwenImageDit.cs:488-496).
     mod = Layers.Linear(model, silu_temb, W("norm_out.weight"), W("norm_out.bias", "wide"))
