@@ -749,8 +749,8 @@ void launch_gemm_generic(const GemmGenericArgs& g, hipStream_t s) {
 // ---- dispatch -----------------------------------------------------------------
 
 enum GemmKind {
-  K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64, K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64, K_F32,
-  K_GENERIC_LINEAR
+  K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64, K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64,
+  K_LDS_256W8, K_LDS_128W8, K_F32, K_GENERIC_LINEAR
 };
 
 // Whether every 16-byte (or 8-byte, int8 GEMV) vector load a kernel makes
@@ -779,13 +779,13 @@ static bool spans_fit(const GemmArgs& a) {
 // round is one workgroup on every slot (256 CUs x the workgroups one CU
 // holds) and a tile's work is BM * BN * (K + K0), K0 its fixed cost in
 // K-equivalents. Rates and K0 are fitted to a sweep of every tile over the
-// DiTs' and the UNet's GEMM shapes on MI355X (rows 154 to 13778, N 640 to
-// 12288, K 640 to 12288): within 0.2% of the best tile on average, 3.5% at
-// worst. Index 0..3: 256x256, 128x128, 64x128, 64x64.
+// DiTs' and the UNet's GEMM shapes on MI355X (34 shapes: rows 154 to 13778,
+// N 640 to 12288, K 640 to 12288): the pick is the best tile on all but one,
+// 0.3% off there. Index 0..3: 256x256 (8 waves), 128x128, 64x128, 64x64.
 static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch, double* model_time = nullptr) {
   struct Tile { int bm, bn, per_cu; double rate; double k0; };
   static const Tile tiles[4] = {
-      {256, 256, 1, 1000.0, 512.0}, {128, 128, 2, 920.0, 128.0}, {64, 128, 3, 700.0, 128.0}, {64, 64, 4, 560.0, 128.0}};
+      {256, 256, 1, 1000.0, 256.0}, {128, 128, 2, 850.0, 128.0}, {64, 128, 3, 700.0, 128.0}, {64, 64, 4, 560.0, 128.0}};
   int best = 0;
   double best_t = 0;
   for (int i = 0; i < 4; i++) {
@@ -825,8 +825,10 @@ static GemmKind choose(const GemmArgs& a) {
       if (!strcmp(pin, "128lds") && a.w_dtype != NDX_I8) return K_LDS_128;
       if (!strcmp(pin, "64x128lds") && a.w_dtype != NDX_I8) return K_LDS_64x128;
       if (!strcmp(pin, "64x64lds") && a.w_dtype != NDX_I8) return K_LDS_64x64;
+      if (!strcmp(pin, "256w8lds") && a.w_dtype != NDX_I8) return K_LDS_256W8;
+      if (!strcmp(pin, "128w8lds") && a.w_dtype != NDX_I8) return K_LDS_128W8;
     }
-    static const GemmKind lds[4] = {K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
+    static const GemmKind lds[4] = {K_LDS_256W8, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
     static const GemmKind reg[4] = {K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64};
     const int t = pick_tile(a.M, a.N, a.K, a.batch);
     return a.w_dtype == NDX_I8 ? reg[t] : lds[t];
@@ -847,6 +849,8 @@ const char* gemm_family(const GemmArgs& a) {
     case K_LDS_128: return "gemm_mfma_lds_128x128";
     case K_LDS_64x128: return "gemm_mfma_lds_64x128";
     case K_LDS_64x64: return "gemm_mfma_lds_64x64";
+    case K_LDS_256W8: return "gemm_mfma_lds_256x256w8";
+    case K_LDS_128W8: return "gemm_mfma_lds_128x128w8";
     case K_F32: return "gemm_f32_mfma_128x128";
     default: return "gemm_linear_generic";
   }
@@ -946,7 +950,7 @@ static GemmArgs conv_gemm_args(const ConvArgs& c) {
 
 const char* conv_family(const ConvArgs& c) {
   switch (conv_choose(conv_gemm_args(c))) {
-    case CK_256: return "conv_mfma_256x256";
+    case CK_256: return "conv_mfma_256x256w8";
     case CK_128: return "conv_mfma_128x128";
     case CK_64x128: return "conv_mfma_64x128";
     default: return "conv_mfma_64x64";
@@ -957,7 +961,7 @@ void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
   const GemmArgs g = conv_gemm_args(c);
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   switch (conv_choose(g)) {
-    case CK_256: launch_mfma_lds<256, 256, 128, 128, true>(g, s); break;
+    case CK_256: launch_mfma_lds<256, 256, 128, 64, true>(g, s); break;
     case CK_128: launch_mfma_lds<128, 128, 64, 64, true>(g, s); break;
     case CK_64x128: launch_mfma_lds<64, 128, 32, 64, true>(g, s); break;
     default: launch_mfma_lds<64, 64, 32, 32, true>(g, s); break;
@@ -965,7 +969,8 @@ void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
 }
 
 static bool is_lds_kind(GemmKind k) {
-  return k == K_LDS_256 || k == K_LDS_128 || k == K_LDS_64x128 || k == K_LDS_64x64;
+  return k == K_LDS_256 || k == K_LDS_128 || k == K_LDS_64x128 || k == K_LDS_64x64 || k == K_LDS_256W8 ||
+         k == K_LDS_128W8;
 }
 
 bool gemm_pair_pays(int64_t M1, int64_t M2, int64_t N, int64_t K, int64_t batch) {
@@ -989,6 +994,8 @@ bool launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s, &b); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s, &b); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s, &b); break;
+    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s, &b); break;
+    case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s, &b); break;
     default: return false;
   }
   return true;
@@ -1019,6 +1026,8 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
+    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s); break;
+    case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
     case K_F32: {
       int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
       int grid = (tiles + 7) / 8 * 8;

@@ -99,7 +99,7 @@ def test_conv_every_tile(device, monkeypatch, tile):
     w = narrow(normal("tw", (300, 128, 3, 3), 1.0 / np.sqrt(128 * 9)), dtype)
     b = narrow(normal("tb", (300,), 0.1), dtype)
     out, families = run_conv(device, dtype, x, w, b, 1, 1)
-    want = {"256": "conv_mfma_256x256", "128": "conv_mfma_128x128", "64x128": "conv_mfma_64x128",
+    want = {"256": "conv_mfma_256x256w8", "128": "conv_mfma_128x128", "64x128": "conv_mfma_64x128",
             "64x64": "conv_mfma_64x64"}[tile]
     assert want in families, families
     assert rel_err(out, oracle.conv2d(x, w, b, 1, 1)) <= TOL[dtype]

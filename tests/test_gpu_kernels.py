@@ -79,7 +79,7 @@ def test_linear_against_oracle(device, M, K, N, B, compute):
 TILE_CASES = [
     (64, 3072, 3072, 1), (40, 1024, 650, 1), (64, 512, 384, 3), (256, 3072, 9216, 1), (128, 3072, 9216, 1),
     (1536, 12288, 3072, 1), (1543, 1024, 8200, 1), (1024, 3072, 12288, 1), (1543, 1024, 10000, 1),
-    (3, 3072, 1000, 2),
+    (2048, 1024, 4096, 1), (3, 3072, 1000, 2),
 ]
 SEEN_FAMILIES = set()
 
@@ -97,7 +97,7 @@ def test_linear_tile_configurations(device, M, K, N, B, int8):
     model.Compiled.SetProfiling(True)
     out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16))[0]
     (family,) = set(model.Compiled.Profile())
-    SEEN_FAMILIES.add(family.replace("_w8", "").replace("_lds", ""))
+    SEEN_FAMILIES.add(family.replace("_w8_", "_").replace("_lds", "").removesuffix("w8"))
     wq = w
     if int8 and w.size >= (1 << 16):
         q, sc = oracle.quantize(w, N)
@@ -108,12 +108,12 @@ def test_linear_tile_configurations(device, M, K, N, B, int8):
 
 
 def test_tile_cases_reached_every_configuration():
-    # The 256x256 tile wins only at the step's own sizes (5376 rows, K 12288):
-    # it is covered pinned, below, and by the step tests.
-    assert SEEN_FAMILIES >= {"gemm_mfma_128x128", "gemm_mfma_64x128", "gemm_mfma_64x64", "gemv"}, SEEN_FAMILIES
+    assert SEEN_FAMILIES >= {"gemm_mfma_256x256", "gemm_mfma_128x128", "gemm_mfma_64x128", "gemm_mfma_64x64",
+                             "gemv"}, SEEN_FAMILIES
 
 
-@pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64", "256lds", "128lds", "64x128lds", "64x64lds"])
+@pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64", "256lds", "128lds", "64x128lds", "64x64lds",
+                                  "256w8lds", "128w8lds"])
 @pytest.mark.parametrize("M,K,N", [(600, 1024, 1000), (1024, 3072, 3072), (77, 320, 2056)])
 def test_linear_every_kernel_variant(device, monkeypatch, tile, M, K, N):
     """Each GEMM kernel, pinned through NDX_GEMM_TILE, against the oracle on
@@ -131,7 +131,8 @@ def test_linear_every_kernel_variant(device, monkeypatch, tile, M, K, N):
     (family,) = set(model.Compiled.Profile())
     assert family.endswith({"256": "mfma_256x256", "128": "mfma_128x128", "64x128": "mfma_64x128",
                             "64x64": "mfma_64x64", "256lds": "lds_256x256", "128lds": "lds_128x128",
-                            "64x128lds": "lds_64x128", "64x64lds": "lds_64x64"}[tile]), family
+                            "64x128lds": "lds_64x128", "64x64lds": "lds_64x64", "256w8lds": "lds_256x256w8",
+                            "128w8lds": "lds_128x128w8"}[tile]), family
     assert rel_err(out, oracle.gelu_tanh(oracle.linear(x, w, b))) <= BF16_TOL
 
 
