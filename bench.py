@@ -188,7 +188,8 @@ def setup_mmdit(args, dev, seed, DT):
         dev.Upload(HostTensor.FromFloats(sin.reshape(1, n, 1, 64))),
     ]
     out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w])]
-    wdesc = "int8 block-32 weights" if args.int8 else f"{args.compute} weights"
+    wdesc = {None: f"{args.compute} weights", "block32": "int8 weights, fp16 scales per 32 columns",
+             "channel": "int8 weights, fp32 scales per output channel"}[args.int8]
     return dict(
         model=model, inputs=inputs, out=out,
         metric="Qwen-Image DiT s/step @1024x1344 (bf16/int8 wts), 1 MI355X; % MFMA peak",
@@ -196,7 +197,7 @@ def setup_mmdit(args, dev, seed, DT):
                              f"(latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), hidden 3072, "
                              f"24x128 heads, MLP 12288, batch 1, {args.compute} compute, {wdesc}"),
                 "blocks": cfg.blocks, "image_tokens": ni, "text_tokens": nt,
-                "weights": "int8" if args.int8 else args.compute},
+                "weights": f"int8-{args.int8}" if args.int8 else args.compute},
         data="synthetic (seeded N(0,1) latent and text, N(0,0.02) bf16 weights made on the GPU)",
         cpu=lambda: cpu_baseline(dev, cfg, seed, ni, nt),
     )
@@ -213,7 +214,7 @@ def setup_anima(args, dev, seed, DT):
     lat, n_ctx = 128, 512
     n = (lat // 2) ** 2
     weights = anima.device_weights(dev, cfg, seed, store)
-    model = anima.build_step_model(dev, cfg, weights, lat, lat, n_ctx, compute, args.int8)
+    model = anima.build_step_model(dev, cfg, weights, lat, lat, n_ctx, compute, bool(args.int8))
     cos, sin = anima.rope_tables(lat // 2, lat // 2, cfg.head_dim)
     half = cfg.head_dim // 2
     inputs = [
@@ -264,7 +265,7 @@ def setup_sdxl(args, dev, seed, DT):
     compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
     B, lat, tokens = 2, 128, 77
     weights = sdxl.device_weights(dev, cfg, seed, compute)
-    model = sdxl.build_unet(dev, cfg, weights, B, lat, lat, tokens, compute, args.int8)
+    model = sdxl.build_unet(dev, cfg, weights, B, lat, lat, tokens, compute, bool(args.int8))
     t = np.tile(sdxl.timestep_embedding([500.0], cfg.block_out[0]), (B, 1)).reshape(B, 1, 1, -1)
     add = np.stack([sdxl.add_conditioning(np.zeros(cfg.pooled_width, np.float32), add_time_dim=cfg.add_time_dim)] * B)
     inputs = [
@@ -293,7 +294,9 @@ def main():
                     help="mmdit (the headline), or the Anima DiT / SDXL UNet steps")
     ap.add_argument("--compute", choices=["bf16", "f32", "f16"], default=None,
                     help="compute type (default bf16; fp16 for sdxl)")
-    ap.add_argument("--int8", action="store_true", help="int8 block-quantised weights")
+    ap.add_argument("--int8", nargs="?", const="block32", default=None, choices=["block32", "channel"],
+                    help="int8 weights: block32 (the reference's BlockQuantizer format, the default) or channel "
+                         "(one fp32 scale per output channel)")
     ap.add_argument("--blocks", type=int, default=None, help="block count (default: the model's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")

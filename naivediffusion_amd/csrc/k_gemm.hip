@@ -520,6 +520,201 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
+// ---- int8 weights, direct to LDS ----------------------------------------------
+//
+// The weight tile travels as int8 (half the bytes of bf16): DMA'd into an
+// LDS staging buffer like the activations, then each thread turns one
+// (row, 32-column block) of it — one scale — into bf16 in the swizzled tile
+// the MFMA loop reads. q * scale is rounded to the compute type, as
+// DmlOps.Dequantize's output is (Graph/ModelBuilder.cs:28-35). Scales are
+// per (row, qblock columns): BlockQuantizer's 32 (fp16), or the whole row
+// (per output channel, fp32).
+template <int BM, int BN, int WM, int WN, typename T, bool SF16>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel(GemmArgs a, int grid) {
+  typedef typename MfmaOp<T>::V V;
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NW = (BM / WM) * (BN / WN), NT = NW * 64;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_LOADS = BM / 8 / NW;    // kilobyte loads of A per wave per tile (8 rows x 128 B)
+  constexpr int W_LOADS = BN / 16 / NW;   // kilobyte loads of W per wave per tile (16 rows x 64 B)
+  static_assert(A_LOADS * 8 * NW == BM && W_LOADS * 16 * NW == BN, "tile rows do not split over the waves");
+  constexpr int A_BYTES = 2 * BM * BK * (int)sizeof(T);
+  constexpr int W8_BYTES = 2 * BN * BK;
+  constexpr int B_BYTES = BN * BK * (int)sizeof(T);
+  constexpr int TILE_BYTES = A_BYTES + W8_BYTES + B_BYTES;
+  constexpr int STAGE_BYTES = NW * 32 * (WN + 4) * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
+  T (*As)[BM * BK] = reinterpret_cast<T (*)[BM * BK]>(smem);
+  int8_t (*W8s)[BN * BK] = reinterpret_cast<int8_t (*)[BN * BK]>(smem + A_BYTES);
+  T* Bs = reinterpret_cast<T*>(smem + A_BYTES + W8_BYTES);
+
+  int tm, tn;
+  if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
+  const int64_t bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  constexpr int ES = (int)sizeof(T);
+
+  const T* A = (const T*)a.a + bidx * a.batch_a;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * ES));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, (uint32_t)(int64_t(a.N - 1) * a.ldw + a.K));
+
+  // A: as the 16-bit kernel (8 rows x 8 swizzled 16-byte chunks per load).
+  const int lrow8 = lane >> 3;
+  const int kchunk = (lane & 7) ^ lrow8;
+  uint32_t a_row[A_LOADS], w_row[W_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; i++) {
+    const int r = (wave * A_LOADS + i) * 8 + lrow8;
+    a_row[i] = m0 + r < a.M ? (uint32_t)(int64_t(m0 + r) * a.lda * ES) : kOutOfRange;
+  }
+  // W: 16 rows x 4 chunks of 16 int8 per load, row-major in LDS.
+  const int wrow16 = lane >> 2, wchunk = lane & 3;
+#pragma unroll
+  for (int i = 0; i < W_LOADS; i++) {
+    const int r = (wave * W_LOADS + i) * 16 + wrow16;
+    w_row[i] = n0 + r < a.N ? (uint32_t)(int64_t(n0 + r) * a.ldw) : kOutOfRange;
+  }
+
+  auto issue_tile = [&](int kt, int buf) {
+    const int k = kt * BK + kchunk * 8;
+    const bool kin = k < a.K;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; i++) {
+      const uint32_t off = (kin && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k * ES) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+    }
+    const int kw = kt * BK + wchunk * 16;
+    const bool kwin = kw < a.K;
+#pragma unroll
+    for (int i = 0; i < W_LOADS; i++) {
+      const uint32_t off = (kwin && w_row[i] != kOutOfRange) ? w_row[i] + uint32_t(kw) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&W8s[buf][(wave * W_LOADS + i) * 16 * BK], 16, off, 0, 0, 0);
+    }
+  };
+
+  // Dequant tasks: (row r, columns [32 h, 32 h + 32)) for task 2 r + h,
+  // one scale each (qblock is a multiple of 32). The scales of tile kt + 1
+  // are loaded during tile kt, before its DMA is issued: vector memory
+  // completes in order, so a scale loaded after the DMA would make the
+  // dequant wait for the whole next tile.
+  // The scale's raw bits (fp16 or fp32 by SF16) travel to the next
+  // iteration unconverted, so nothing waits on the load until then.
+  constexpr int TPT = (2 * BN + NT - 1) / NT;  // tasks per thread
+  auto load_scales = [&](int kt, uint32_t (&raw)[TPT]) {
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+      const int task = tid + t * NT, dr = task >> 1, k0 = kt * BK + (task & 1) * 32;
+      const int64_t i = int64_t(n0 + dr) * a.lds + k0 / a.qblock;
+      const bool in = task < 2 * BN && n0 + dr < a.N && k0 < a.K;
+      if (SF16) raw[t] = in ? (uint32_t)((const uint16_t*)a.scales)[i] : 0u;
+      else raw[t] = in ? ((const uint32_t*)a.scales)[i] : 0u;
+    }
+  };
+  auto dequant = [&](int buf, const float (&scs)[TPT]) {
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+      const int task = tid + t * NT;
+      // (A branch here only where the tasks do not fill the threads: a
+      // divergent branch before the LDS reads makes the compiler wait for
+      // the next tile's DMA.)
+      if (NT * TPT != 2 * BN && task >= 2 * BN) break;
+      const int dr = task >> 1, dh = task & 1;
+      const float sc = scs[t];
+      const uint4 q0 = *(const uint4*)&W8s[buf][dr * BK + dh * 32];
+      const uint4 q1 = *(const uint4*)&W8s[buf][dr * BK + dh * 32 + 16];
+      const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        T h[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int v = (int)(int8_t)((w[2 * c + e / 4] >> (8 * (e & 3))) & 0xff);
+          h[e] = (T)((float)v * sc);
+        }
+        *(uint4*)&Bs[swz(dr, dh * 4 + c)] = *(const uint4*)h;
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int KT = (a.K + BK - 1) / BK;
+  uint32_t sc_next[TPT];
+  load_scales(0, sc_next);
+  issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    // This tile's scales arrived with the previous tile's loads: convert
+    // them before this iteration issues any load.
+    float sc_cur[TPT];
+#pragma unroll
+    for (int t = 0; t < TPT; t++)
+      sc_cur[t] = SF16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)sc_next[t]) : __uint_as_float(sc_next[t]);
+    // Dequantise before the next tile's DMA is in flight (an LDS read after
+    // it would wait for it), then issue that DMA to overlap the MFMAs. The
+    // barrier waits only for the LDS writes (lgkmcnt 0), not the DMA.
+    dequant(cur, sc_cur);
+    load_scales(kt + 1, sc_next);
+    issue_tile(kt + 1, cur ^ 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    V af[2][TM], bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bs[swz(wn * WN + j * 32 + lrow, lhalf)];
+#pragma unroll
+    for (int s = 0; s < BK / 16; s++) {
+      const int p = s & 1;
+      if (s + 1 < BK / 16) {
+        const int c = 2 * (s + 1) + lhalf;
+#pragma unroll
+        for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, c)];
+#pragma unroll
+        for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bs[swz(wn * WN + j * 32 + lrow, c)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[p][i], bf[p][j], acc[i][j]);
+    }
+    // Each step's MFMAs with the next step's fragment reads threaded
+    // between them, as in the 16-bit kernel.
+    constexpr int NF = TM + TN, NM = TM * TN;
+    __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
+#pragma unroll
+    for (int s = 0; s < BK / 16 - 1; s++) {
+      if (NM >= NF) {
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+          __builtin_amdgcn_sched_group_barrier(0x0008, NM / NF, 0);
+          __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
+  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+}
+
 // ---- fp32 -------------------------------------------------------------------
 
 static constexpr int BK32 = 32;
@@ -750,7 +945,7 @@ void launch_gemm_generic(const GemmGenericArgs& g, hipStream_t s) {
 
 enum GemmKind {
   K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64, K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64,
-  K_LDS_256W8, K_LDS_128W8, K_F32, K_GENERIC_LINEAR
+  K_LDS_256W8, K_LDS_128W8, K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64, K_F32, K_GENERIC_LINEAR
 };
 
 // Whether every 16-byte (or 8-byte, int8 GEMV) vector load a kernel makes
@@ -827,11 +1022,20 @@ static GemmKind choose(const GemmArgs& a) {
       if (!strcmp(pin, "64x64lds") && a.w_dtype != NDX_I8) return K_LDS_64x64;
       if (!strcmp(pin, "256w8lds") && a.w_dtype != NDX_I8) return K_LDS_256W8;
       if (!strcmp(pin, "128w8lds") && a.w_dtype != NDX_I8) return K_LDS_128W8;
+      if (a.w_dtype == NDX_I8 && a.qblock % 32 == 0) {
+        if (!strcmp(pin, "256w8lds") || !strcmp(pin, "256lds")) return K_W8_256W8;
+        if (!strcmp(pin, "128lds")) return K_W8_128;
+        if (!strcmp(pin, "64x128lds")) return K_W8_64x128;
+        if (!strcmp(pin, "64x64lds")) return K_W8_64x64;
+      }
     }
     static const GemmKind lds[4] = {K_LDS_256W8, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
+    static const GemmKind w8[4] = {K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64};
     static const GemmKind reg[4] = {K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64};
     const int t = pick_tile(a.M, a.N, a.K, a.batch);
-    return a.w_dtype == NDX_I8 ? reg[t] : lds[t];
+    if (a.w_dtype != NDX_I8) return lds[t];
+    // The direct-to-LDS int8 kernel takes one scale per 32 columns.
+    return a.qblock % 32 == 0 ? w8[t] : reg[t];
   }
   if (a.a_dtype == NDX_F32 && a.K % 8 == 0) return K_F32;
   return K_GENERIC_LINEAR;
@@ -851,6 +1055,10 @@ const char* gemm_family(const GemmArgs& a) {
     case K_LDS_64x64: return "gemm_mfma_lds_64x64";
     case K_LDS_256W8: return "gemm_mfma_lds_256x256w8";
     case K_LDS_128W8: return "gemm_mfma_lds_128x128w8";
+    case K_W8_256W8: return "gemm_w8_lds_256x256w8";
+    case K_W8_128: return "gemm_w8_lds_128x128";
+    case K_W8_64x128: return "gemm_w8_lds_64x128";
+    case K_W8_64x64: return "gemm_w8_lds_64x64";
     case K_F32: return "gemm_f32_mfma_128x128";
     default: return "gemm_linear_generic";
   }
@@ -968,6 +1176,21 @@ void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
   }
 }
 
+template <int BM, int BN, int WM, int WN>
+static void launch_w8_lds(const GemmArgs& a, hipStream_t s) {
+  int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  int grid = (tiles + 7) / 8 * 8;
+  dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
+  const bool f16s = a.s_dtype == NDX_F16;
+  if (a.a_dtype == NDX_BF16) {
+    if (f16s) hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, __bf16, true>), g, b, 0, s, a, grid);
+    else hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, __bf16, false>), g, b, 0, s, a, grid);
+  } else {
+    if (f16s) hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, _Float16, true>), g, b, 0, s, a, grid);
+    else hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, _Float16, false>), g, b, 0, s, a, grid);
+  }
+}
+
 static bool is_lds_kind(GemmKind k) {
   return k == K_LDS_256 || k == K_LDS_128 || k == K_LDS_64x128 || k == K_LDS_64x64 || k == K_LDS_256W8 ||
          k == K_LDS_128W8;
@@ -1028,6 +1251,10 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
     case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s); break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
+    case K_W8_256W8: launch_w8_lds<256, 256, 128, 64>(a, s); break;
+    case K_W8_128: launch_w8_lds<128, 128, 64, 64>(a, s); break;
+    case K_W8_64x128: launch_w8_lds<64, 128, 32, 64>(a, s); break;
+    case K_W8_64x64: launch_w8_lds<64, 64, 32, 32>(a, s); break;
     case K_F32: {
       int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
       int grid = (tiles + 7) / 8 * 8;

@@ -454,6 +454,11 @@ class ModelBuilder:
         """Weight for data already on the device; the graph takes it over."""
         return self.Graph._new("ndx_graph_weight_device", tensor.take(), int(rows))
 
+    def WeightInt8(self, q: DeviceTensor, scales: DeviceTensor, block: int) -> Expression:
+        """A pre-quantised weight (Device.QuantizeInt8's output); the graph
+        takes both tensors over."""
+        return self.Graph._new("ndx_graph_weight_int8", q.take(), scales.take(), int(block))
+
     def ConstantOnDevice(self, tensor: DeviceTensor) -> Expression:
         return self.Graph._new("ndx_graph_constant_device", tensor.take())
 

@@ -150,10 +150,13 @@ def time_embedding(t: float, width: int) -> np.ndarray:
 
 
 class _W:
-    """Registers each named weight once in a builder."""
+    """Registers each named weight once in a builder. With per_channel the
+    matrices are quantised to int8 on the device with one fp32 scale per
+    output row (block = the row) and handed over pre-quantised."""
 
-    def __init__(self, model: ModelBuilder, weights: dict, compute: HostDataType):
+    def __init__(self, model: ModelBuilder, weights: dict, compute: HostDataType, per_channel: bool = False):
         self.model, self.weights, self.compute = model, weights, compute
+        self.per_channel = per_channel
         self.cache = {}
 
     def __call__(self, name: str, kind: str = "weight"):
@@ -163,7 +166,10 @@ class _W:
         m = self.model
         if isinstance(w, DeviceTensor):
             shape = w.Shape
-            if kind == "weight" and len(shape) == 2:
+            if kind == "weight" and len(shape) == 2 and self.per_channel and shape[0] * shape[1] >= (1 << 16):
+                q, sc = m.Device.QuantizeInt8(w, shape[1], HostDataType.Float32)
+                e = m.WeightInt8(q, sc, shape[1])
+            elif kind == "weight" and len(shape) == 2:
                 e = m.WeightOnDevice(w, shape[0])
             else:
                 e = m.ConstantOnDevice(w)
@@ -258,7 +264,7 @@ def build_block_model(device: Device, cfg: MmditConfig, weights: dict, batch: in
 
 
 def build_step_model(device: Device, cfg: MmditConfig, weights: dict, batch: int, n_txt: int, latent_h: int,
-                     latent_w: int, compute: HostDataType, int8: bool = False, two_streams: bool = True):
+                     latent_w: int, compute: HostDataType, int8=False, two_streams: bool = True):
     """The full denoiser step as one compiled model (every GraphChain cut of
     the reference is a no-op here: everything is resident). Inputs: latent
     [B, C, H, W] fp32, text [B, 1, Nt, text_dim] fp32, the time sinusoid
@@ -266,8 +272,11 @@ def build_step_model(device: Device, cfg: MmditConfig, weights: dict, batch: int
     [B, C, H, W] fp32."""
     D, C, p = cfg.width, cfg.latent_channels, cfg.patch
     n_img = (latent_h // p) * (latent_w // p)
-    model = ModelBuilder(device, compute, int8)
-    W = _W(model, weights, compute)
+    # int8: False, True / "block32" (the reference's BlockQuantizer format,
+    # quantised by the builder) or "channel" (one fp32 scale per output row).
+    per_channel = int8 == "channel"
+    model = ModelBuilder(device, compute, bool(int8) and not per_channel)
+    W = _W(model, weights, compute, per_channel)
     latent = model.Placeholder([batch, C, latent_h, latent_w], HostDataType.Float32)
     text = model.Placeholder([batch, 1, n_txt, cfg.text_dim], HostDataType.Float32)
     tsin = model.Placeholder([batch, 1, 1, cfg.time_dim], HostDataType.Float32)

@@ -185,6 +185,18 @@ class Device:
         call("ndx_tensor_fill_normal", t.handle, ctypes.c_uint64(seed & (2**64 - 1)), mean, std)
         return t
 
+    def QuantizeInt8(self, weight: "DeviceTensor", block: int = 32,
+                     scaleType: HostDataType = HostDataType.Float16) -> tuple:
+        """BlockQuantizer.Quantize (Tensors/BlockQuantizer.cs:34-101) on the
+        device: weight [rows, cols] -> (q int8 [rows, cols], scales [rows,
+        cols / block] of scaleType). block 32 with Float16 scales is the
+        reference's format; block = cols with Float32 is per output channel."""
+        rows, cols = weight.Shape[0], int(np.prod(weight.Shape[1:]))
+        q = self.Empty(HostDataType.Int8, [rows, cols])
+        s = self.Empty(scaleType, [rows, cols // block])
+        call("ndx_quantize_block_int8_device", weight.handle, int(block), int(scaleType), q.handle, s.handle)
+        return q, s
+
     def Dispose(self):
         if self._h is not None:
             call("ndx_device_destroy", self._h)

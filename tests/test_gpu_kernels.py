@@ -186,6 +186,45 @@ def test_int8_linear_against_oracle(device, compute, M):
     assert rel_err(out, oracle.linear(x, w)) <= BF16_TOL
 
 
+@pytest.mark.parametrize("tile", ["auto", "256w8lds", "128lds", "64x128lds", "64x64lds", "256"])
+@pytest.mark.parametrize("fmt", ["block32", "channel"])
+def test_int8_kernels_every_tile(device, monkeypatch, tile, fmt):
+    """The int8 GEMMs (direct-to-LDS with the cooperative dequant, and the
+    register-staged one pinned as "256") on ragged shapes, with the
+    reference's block-32 fp16 scales and with per-output-channel fp32 scales
+    (Device.QuantizeInt8 + ModelBuilder.WeightInt8)."""
+    print(f"[gpu] int8 {fmt} tile {tile}", flush=True)
+    if tile != "auto":
+        monkeypatch.setenv("NDX_GEMM_TILE", tile)
+    M, K, N = 700, 1024, 1000
+    x = bf(normal("ix", (1, 1, M, K)))
+    w = bf(normal("iw", (N, K), 0.02))
+    b = bf(normal("ib", (N,), 0.02))
+    if fmt == "block32":
+        model = nd.ModelBuilder(device, DT.BFloat16, int8Weights=True)
+        wv = HostTensor.FromFloats(w)
+        q, sc = oracle.quantize(w, N)
+        deq = (q.astype(np.float32).reshape(N, K // 32, 32) * oracle.f16_bits_to_f32(sc)[:, :, None]).reshape(N, K)
+    else:
+        model = nd.ModelBuilder(device, DT.BFloat16)
+        wt = device.Upload(HostTensor.FromFloats(w).ConvertTo(DT.BFloat16))
+        qd, sd = device.QuantizeInt8(wt, K, DT.Float32)
+        q, sc = oracle.quantize(w, N, K, fp16_scales=False)
+        # The device quantiser is bit-exact with the oracle in this format too.
+        assert np.array_equal(qd.Download().Data, q) and np.array_equal(sd.Download().Data.ravel(), sc.ravel())
+        wv = model.WeightInt8(qd, sd, K)
+        deq = q.astype(np.float32) * np.asarray(sc, np.float32).reshape(N, 1)
+    xin = model.Placeholder([1, 1, M, K])
+    model.Compile([Layers.Linear(model, xin, wv, HostTensor.FromFloats(b), activation="gelu_tanh")])
+    model.Compiled.SetProfiling(True)
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16))[0]
+    (family,) = set(model.Compiled.Profile())
+    assert "_w8_" in family, family
+    if tile not in ("auto", "256"):
+        assert "w8_lds" in family, family
+    assert rel_err(out, oracle.gelu_tanh(oracle.linear(x, deq, b))) <= BF16_TOL
+
+
 def test_device_quantizer_is_bit_exact_with_the_oracle(device):
     w = bf(normal("dq", (640, 3072), 0.02))
     wt = device.Upload(HostTensor.FromFloats(w).ConvertTo(DT.BFloat16))
