@@ -28,6 +28,7 @@ from typing import Dict
 import numpy as np
 
 from . import rng
+from .chain import GraphChain
 from .graph import PATCH_CHANNEL_FIRST, PATCH_CHANNEL_LAST, ModelBuilder, Ops
 from .layers import Layers, Transformer
 from .tensors import Device, DeviceTensor, HostDataType, HostTensor, bf16_to_f32, f32_to_bf16
@@ -210,50 +211,76 @@ def build_block(model: ModelBuilder, W: WeightSet, i: int, cfg: AnimaConfig, x, 
     return Layers.Linear(model, f, W(f"{p}.mlp.layer2.weight"), gate=g, residual=x)
 
 
-def _inputs(model: ModelBuilder, cfg: AnimaConfig, n_tokens: int, n_ctx: int, latent_h: int, latent_w: int):
-    F32 = HostDataType.Float32
-    latent = model.Placeholder([1, cfg.latent_channels, latent_h, latent_w], F32)
-    time = model.Placeholder([1, 1, 1, cfg.width], F32)
-    context = model.Placeholder([1, 1, n_ctx, cfg.context_width], F32)
-    cos = model.Placeholder([1, n_tokens, 1, cfg.head_dim // 2], F32)
-    sin = model.Placeholder([1, n_tokens, 1, cfg.head_dim // 2], F32)
-    return latent, time, context, cos, sin
+# Names of the values the step's chain carries (AnimaDit.cs:37-45; the
+# latent replaces the reference's host-made patches: it is patchified on the
+# device).
+LATENT, TIME, CONTEXT, COS, SIN = "latent", "time", "context", "cos", "sin"
+X, TEMB, LORA, OUT = "x", "temb", "lora", "out"
 
 
-def build_step_model(device: Device, cfg: AnimaConfig, weights: dict, latent_h: int, latent_w: int, n_ctx: int,
-                     compute: HostDataType, int8: bool = False, blocks: int = None):
-    """The whole denoiser step as one compiled model (AnimaDit.Build,
-    :360-404; every GraphChain cut is a no-op here). Inputs: latent [1, 16,
-    H, W], the time sinusoid [1, 1, 1, D] (Sinusoid(sigma, D)), context [1,
-    1, Nc, Cw], cos, sin [1, N, 1, d/2], all fp32. Output: the flow [1, 16,
-    H, W] fp32."""
+def build_step_chain(device: Device, cfg: AnimaConfig, weights: dict, latent_h: int, latent_w: int, n_ctx: int,
+                     compute: HostDataType, int8: bool = False, blocks: int = None) -> GraphChain:
+    """The denoiser step as a GraphChain (AnimaDit.Build, :360-404): the
+    embeddings, one link per block, the final layer. Inputs by name: latent
+    [1, 16, H, W], time [1, 1, 1, D] (Sinusoid(sigma, D)), context [1, 1,
+    Nc, Cw], cos, sin [1, N, 1, d/2], all fp32. Result: the flow [1, 16, H,
+    W] fp32. The links compile into one model."""
     D, C, p = cfg.width, cfg.latent_channels, cfg.patch
     n = (latent_h // p) * (latent_w // p)
     blocks = cfg.blocks if blocks is None else blocks
-    store = compute if compute != HostDataType.Float32 else HostDataType.Float16
-    model = ModelBuilder(device, store, int8)
-    W = WeightSet(model, weights, compute, device)
-    latent, time, context, cos, sin = _inputs(model, cfg, n, n_ctx, latent_h, latent_w)
+    F32 = HostDataType.Float32
+    store = compute if compute != F32 else HostDataType.Float16
+    chain = GraphChain(device, store, None, int8)
+    try:
+        model = chain.Current
+        W = WeightSet(model, weights, compute, device)
+        chain.Input(LATENT, [1, C, latent_h, latent_w], F32)
+        chain.Input(TIME, [1, 1, 1, D], F32)
+        chain.Input(CONTEXT, [1, 1, n_ctx, cfg.context_width], F32)
+        chain.Input(COS, [1, n, 1, cfg.head_dim // 2], F32)
+        chain.Input(SIN, [1, n, 1, cfg.head_dim // 2], F32)
 
-    # Embeddings, wide: the sixteen real channels' columns of the patch
-    # embedding (RealChannelColumns, :251-262), the normed time and the
-    # shared adaLN term through the time embedder.
-    x = Layers.Linear(model, Ops.Patchify(latent, p, PATCH_CHANNEL_FIRST),
-                      W.columns("x_embedder.proj.1.weight", C * p * p))
-    temb = Layers.RmsNorm(model, time, W("t_embedding_norm.weight", "wide"), cfg.eps)
-    lora = Layers.Linear(model, Layers.Silu(Layers.Linear(model, time, W("t_embedder.1.linear_1.weight"))),
-                         W("t_embedder.1.linear_2.weight"))
-    silu_temb = Layers.Silu(temb)
-    ctx = context if compute == HostDataType.Float32 else Layers.Cast(context, compute)
-    for i in range(blocks):
-        x = build_block(model, W, i, cfg, x, silu_temb, lora, ctx, cos, sin, compute)
-    sh, sc = modulation(model, W, "final_layer.adaln_modulation", silu_temb, lora, 2, D)
-    y = Transformer.Modulate(x, sh, sc, cfg.eps, HostDataType.Float32)
-    out = Layers.Linear(model, y, W("final_layer.linear.weight"))
-    flow = Ops.Unpatchify(out, p, C, latent_h, latent_w, PATCH_CHANNEL_LAST)
-    model.Compile([flow])
-    W.release()
-    return model
+        # Embeddings, wide: the sixteen real channels' columns of the patch
+        # embedding (RealChannelColumns, :251-262), the normed time and the
+        # shared adaLN term through the time embedder. The blocks read
+        # silu(temb); it is carried under the temb name.
+        chain.Set(X, Layers.Linear(model, Ops.Patchify(chain.Get(LATENT), p, PATCH_CHANNEL_FIRST),
+                                   W.columns("x_embedder.proj.1.weight", C * p * p)))
+        chain.Drop(LATENT)
+        time = chain.Get(TIME)
+        chain.Set(TEMB, Layers.Silu(Layers.RmsNorm(model, time, W("t_embedding_norm.weight", "wide"), cfg.eps)))
+        chain.Set(LORA, Layers.Linear(model, Layers.Silu(Layers.Linear(model, time,
+                                                                        W("t_embedder.1.linear_1.weight"))),
+                                      W("t_embedder.1.linear_2.weight")))
+        chain.Drop(TIME)
+        if compute != F32:
+            chain.Set(CONTEXT, Layers.Cast(chain.Get(CONTEXT), compute))
+        chain.Cut()
+
+        for i in range(blocks):
+            chain.Set(X, build_block(model, W, i, cfg, chain.Get(X), chain.Get(TEMB), chain.Get(LORA),
+                                     chain.Get(CONTEXT), chain.Get(COS), chain.Get(SIN), compute))
+            chain.Cut()
+
+        sh, sc = modulation(model, W, "final_layer.adaln_modulation", chain.Get(TEMB), chain.Get(LORA), 2, D)
+        y = Transformer.Modulate(chain.Get(X), sh, sc, cfg.eps, F32)
+        out = Layers.Linear(model, y, W("final_layer.linear.weight"))
+        chain.Set(OUT, Ops.Unpatchify(out, p, C, latent_h, latent_w, PATCH_CHANNEL_LAST))
+        for name in (X, TEMB, LORA, CONTEXT, COS, SIN):
+            chain.Drop(name)
+        chain.Finish(OUT)
+        W.release()
+    except BaseException:
+        chain.Dispose()
+        raise
+    return chain
+
+
+def build_step_model(device: Device, cfg: AnimaConfig, weights: dict, latent_h: int, latent_w: int, n_ctx: int,
+                     compute: HostDataType, int8: bool = False, blocks: int = None) -> ModelBuilder:
+    """The step chain's compiled model, its inputs bound in the order
+    latent, time, context, cos, sin."""
+    return build_step_chain(device, cfg, weights, latent_h, latent_w, n_ctx, compute, int8, blocks).Current
 
 
 def build_block_model(device: Device, cfg: AnimaConfig, weights: dict, n_tokens: int, n_ctx: int,
@@ -294,7 +321,7 @@ class AnimaDit:
             from ._lib import ArgumentError
             raise ArgumentError(f"{width}x{height} does not divide into 16-pixel patches")
         self.context_rows = context_rows
-        self.model = build_step_model(device, cfg, weights, self.latent_h, self.latent_w, context_rows, compute, int8)
+        self.chain = build_step_chain(device, cfg, weights, self.latent_h, self.latent_w, context_rows, compute, int8)
         self.cos, self.sin = rope_tables(self.latent_h // cfg.patch, self.latent_w // cfg.patch, cfg.head_dim)
 
     @property
@@ -306,11 +333,23 @@ class AnimaDit:
         n, half = self.cos.shape
         ctx = np.asarray(conditioning["context"], np.float32).reshape(1, 1, self.context_rows, cfg.context_width)
         t = Transformer.Sinusoid(float(sigma), cfg.width).reshape(1, 1, 1, cfg.width)
-        ins = [latent.ConvertTo(HostDataType.Float32).Reshape(1, cfg.latent_channels, self.latent_h, self.latent_w),
-               HostTensor.FromFloats(t), HostTensor.FromFloats(ctx),
-               HostTensor.FromFloats(self.cos.reshape(1, n, 1, half)),
-               HostTensor.FromFloats(self.sin.reshape(1, n, 1, half))]
-        return self.model.Run(*ins)[0]
+        return self.chain.Run({
+            LATENT: latent.Reshape(1, cfg.latent_channels, self.latent_h, self.latent_w),
+            TIME: HostTensor.FromFloats(t), CONTEXT: HostTensor.FromFloats(ctx),
+            COS: HostTensor.FromFloats(self.cos.reshape(1, n, 1, half)),
+            SIN: HostTensor.FromFloats(self.sin.reshape(1, n, 1, half))})
+
+    @property
+    def PersistentBytes(self) -> int:
+        return self.chain.PersistentBytes
+
+    @property
+    def TemporaryBytes(self) -> int:
+        return self.chain.TemporaryBytes
+
+    @property
+    def GraphCount(self) -> int:
+        return self.chain.LinkCount
 
     def Dispose(self):
-        self.model.Dispose()
+        self.chain.Dispose()
