@@ -88,24 +88,58 @@ __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t b, int r
   store_f(a.c, a.c_dtype, b * a.batch_c + int64_t(row) * a.ldc + col, v);
 }
 
-// The epilogue of four consecutive outputs (row, col..col+3): bias,
-// activation or (gated) residual, then one 8- or 16-byte store when the
-// row is aligned for it.
-__device__ __forceinline__ void epilogue_four(const GemmArgs& a, int64_t b, int row, int col, float4 acc,
-                                              bool vec_ok) {
-  if (row >= a.M || col >= a.N) return;
-  float v[4] = {acc.x, acc.y, acc.z, acc.w};
-  const bool full = col + 3 < a.N;
-  if (a.bias) {
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      if (full || col + e < a.N) v[e] += load_f(a.bias, a.bias_dtype, col + e);
+// Four consecutive values p[off .. off + 4) widened to fp32, in one 16-byte
+// (fp32) or 8-byte (16-bit) load; the address must allow it.
+__device__ __forceinline__ float4 load4_vec(const void* p, int dt, int64_t off) {
+  if (dt == NDX_F32) return *(const float4*)((const float*)p + off);
+  const uint2 u = dt == NDX_BF16 ? *(const uint2*)((const __bf16*)p + off) : *(const uint2*)((const _Float16*)p + off);
+  if (dt == NDX_BF16) {
+    const __bf16* h = (const __bf16*)&u;
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
   }
-  if (a.row_bias) {
-    const float rb = load_f(a.row_bias, a.row_bias_dtype, row);
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] += rb;
+  const _Float16* h = (const _Float16*)&u;
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+// Stores four consecutive outputs in one 16-byte (fp32) or 8-byte (16-bit)
+// store; the address must allow it.
+__device__ __forceinline__ void store4_vec(void* p, int dt, int64_t off, const float (&v)[4]) {
+  if (dt == NDX_F32) {
+    *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (dt == NDX_BF16) {
+    __bf16 h[4] = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    *(uint2*)((__bf16*)p + off) = *(const uint2*)h;
+  } else {
+    _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *(uint2*)((_Float16*)p + off) = *(const uint2*)h;
   }
+}
+
+// The linear epilogues of four consecutive outputs with every input already
+// in registers and every address vector-aligned: bias (per column, plus rb
+// per row), then the (gated) residual r + g * y with y rounded to the
+// product's type, or nothing more.
+__device__ __forceinline__ void epilogue_fast(const GemmArgs& a, int64_t b, int row, int col, float4 acc, float4 bias,
+                                              float rb, float4 gate, float4 res) {
+  if (row >= a.M) return;
+  float v[4] = {acc.x + bias.x + rb, acc.y + bias.y + rb, acc.z + bias.z + rb, acc.w + bias.w + rb};
+  if (a.epilogue == EPI_GATED_RESIDUAL || a.epilogue == EPI_RESIDUAL) {
+    const float g[4] = {gate.x, gate.y, gate.z, gate.w}, r[4] = {res.x, res.y, res.z, res.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = r[e] + g[e] * round_to(v[e], a.a_dtype);
+  }
+  store4_vec(a.c, a.c_dtype, b * a.batch_c + int64_t(row) * a.ldc + col, v);
+}
+
+// Any epilogue of outputs (row, col .. col + n), n <= 4, reading what it
+// needs per element: bias and gate come in (per column), the row bias and
+// the residual are read here; GELU-tanh, GELU or SiLU, or the (gated)
+// residual; vector stores where all four are there and vec allows.
+__device__ __forceinline__ void epilogue_any(const GemmArgs& a, int64_t b, int row, int col, int n, float4 acc,
+                                             float4 bias, float4 gate, bool vec) {
+  if (row >= a.M || n <= 0) return;
+  const float rb = a.row_bias ? load_f(a.row_bias, a.row_bias_dtype, row) : 0.f;
+  float v[4] = {acc.x + bias.x + rb, acc.y + bias.y + rb, acc.z + bias.z + rb, acc.w + bias.w + rb};
   const int ep = a.epilogue;
   if (ep == EPI_GELU_TANH) {
 #pragma unroll
@@ -117,82 +151,136 @@ __device__ __forceinline__ void epilogue_four(const GemmArgs& a, int64_t b, int 
 #pragma unroll
     for (int e = 0; e < 4; e++) v[e] = silu_f(v[e]);
   } else if (ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL) {
+    const float g[4] = {gate.x, gate.y, gate.z, gate.w};
     const int64_t ro = b * a.batch_r + int64_t(row) * a.ldr + col;
-    float r[4], g[4] = {1.f, 1.f, 1.f, 1.f};
-    if (full && vec_ok && a.r_dtype == NDX_F32) {
-      float4 rv = *(const float4*)((const float*)a.resid + ro);
-      r[0] = rv.x; r[1] = rv.y; r[2] = rv.z; r[3] = rv.w;
-    } else {
 #pragma unroll
-      for (int e = 0; e < 4; e++) r[e] = (full || col + e < a.N) ? load_f(a.resid, a.r_dtype, ro + e) : 0.f;
-    }
-    if (ep == EPI_GATED_RESIDUAL) {
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        g[e] = (full || col + e < a.N) ? load_f(a.gate, a.gate_dtype, b * a.batch_gate + col + e) : 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) v[e] = r[e] + g[e] * round_to(v[e], a.a_dtype);
+    for (int e = 0; e < 4; e++)
+      if (e < n) v[e] = load_f(a.resid, a.r_dtype, ro + e) + g[e] * round_to(v[e], a.a_dtype);
   }
   const int64_t co = b * a.batch_c + int64_t(row) * a.ldc + col;
-  if (full && vec_ok) {
-    if (a.c_dtype == NDX_F32) {
-      *(float4*)((float*)a.c + co) = make_float4(v[0], v[1], v[2], v[3]);
-      return;
-    }
-    if (a.c_dtype == NDX_BF16) {
-      __bf16 h[4] = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-      *(uint2*)((__bf16*)a.c + co) = *(const uint2*)h;
-      return;
-    }
-    if (a.c_dtype == NDX_F16) {
-      _Float16 h[4] = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-      *(uint2*)((_Float16*)a.c + co) = *(const uint2*)h;
-      return;
-    }
+  if (n >= 4 && vec) {
+    store4_vec(a.c, a.c_dtype, co, v);
+    return;
   }
 #pragma unroll
   for (int e = 0; e < 4; e++)
-    if (col + e < a.N) store_f(a.c, a.c_dtype, co + e, v[e]);
+    if (e < n) store_f(a.c, a.c_dtype, co + e, v[e]);
 }
 
-// Whether the output (and residual) rows allow 16-byte vector access at
-// every multiple-of-4 column.
-__device__ __forceinline__ bool epilogue_vec_ok(const GemmArgs& a) {
-  const int cs = dtype_size(a.c_dtype);
-  bool ok = (uintptr_t)a.c % 16 == 0 && (a.ldc * cs) % 16 == 0 && (a.batch_c * cs) % 16 == 0;
-  if (a.resid) {
-    const int rs = dtype_size(a.r_dtype);
-    ok = ok && (uintptr_t)a.resid % 16 == 0 && (a.ldr * rs) % 16 == 0 && (a.batch_r * rs) % 16 == 0;
+__device__ __forceinline__ bool aligned16(const void* p, int64_t elems_a, int64_t elems_b, int es) {
+  return (uintptr_t)p % 16 == 0 && (elems_a * es) % 16 == 0 && (elems_b * es) % 16 == 0;
+}
+
+// Up to four per-column values p[off .. off + n) (zeros past n).
+__device__ __forceinline__ float4 load_cols(const void* p, int dt, int64_t off, int n, bool vec) {
+  if (n >= 4 && vec) return load4_vec(p, dt, off);
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < n && e < 4; e++) v[e] = load_f(p, dt, off + e);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// What every slice of a wave's epilogue shares: the lane's columns, the
+// bias and gate of those columns, and which epilogue path runs.
+struct EpiLane {
+  int col, n, c4, rl0;
+  float4 bias, gate;
+  bool fast, out_vec;
+};
+
+// One 32-row slice (accumulator row block i of the wave) through LDS, so
+// the epilogue walks rows of four consecutive outputs and every global
+// store is a vector. On the fast path (a linear epilogue, every column of
+// the wave in range, aligned rows) the loop is unrolled so that the slice's
+// residual and row-bias loads all go out before its first store, and their
+// latency is paid once per slice rather than once per row. Anything else
+// (the activations, whose code is long and which read nothing per row;
+// ragged or unaligned edges) runs a rolled loop.
+template <int TN, int WN>
+__device__ __forceinline__ void epilogue_slice(const GemmArgs& a, int64_t bidx, const EpiLane& L,
+                                               f32x16 (&acc)[TN], float* stage, int row0) {
+  constexpr int CS = WN + 4;
+  constexpr int C4 = WN / 4;        // four-column groups in a wave's row
+  constexpr int RSTEP = 64 / C4;    // rows one pass of the wave covers
+  constexpr int IT = 32 / RSTEP;    // passes per 32-row slice
+  static_assert(64 % C4 == 0 && 32 % RSTEP == 0, "wave columns do not tile the slice");
+  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
+  const bool residual = a.epilogue == EPI_GATED_RESIDUAL || a.epilogue == EPI_RESIDUAL;
+  float4 res[IT];
+  float rb[IT];
+  if (L.fast) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) {
+      const int row = row0 + L.rl0 + t * RSTEP;
+      const bool in = row < a.M;
+      res[t] = (residual && in) ? load4_vec(a.resid, a.r_dtype, bidx * a.batch_r + int64_t(row) * a.ldr + L.col)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      rb[t] = (a.row_bias && in) ? load_f(a.row_bias, a.row_bias_dtype, row) : 0.f;
+    }
   }
-  return ok;
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[j][r];
+  __syncthreads();
+  if (L.fast) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) {
+      const int rl = L.rl0 + t * RSTEP;
+      const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
+      epilogue_fast(a, bidx, row0 + rl, L.col, v, L.bias, rb[t], L.gate, res[t]);
+    }
+  } else {
+#pragma unroll 1
+    for (int t = 0; t < IT; t++) {
+      const int rl = L.rl0 + t * RSTEP;
+      const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
+      epilogue_any(a, bidx, row0 + rl, L.col, L.n, v, L.bias, L.gate, L.out_vec);
+    }
+  }
+  __syncthreads();
+}
+
+// Slices I .. TM - 1, expanded at compile time so every accumulator index
+// is a constant (a runtime index would put the accumulators in scratch).
+template <int I, int TM, int TN, int WN>
+__device__ __forceinline__ void epilogue_slices(const GemmArgs& a, int64_t bidx, const EpiLane& L,
+                                                f32x16 (&acc)[TM][TN], float* stage, int row0) {
+  if constexpr (I < TM) {
+    epilogue_slice<TN, WN>(a, bidx, L, acc[I], stage, row0 + I * 32);
+    epilogue_slices<I + 1, TM, TN, WN>(a, bidx, L, acc, stage, row0);
+  }
 }
 
 // Writes the accumulators of one wave (TM x TN tiles of 32 x 32, the MFMA
 // layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4)
-// through LDS one 32-row slice at a time, so the epilogue walks rows of
-// four consecutive outputs and every global store is a vector. stage must
-// hold 32 x (WN + 4) floats for each wave and be free (the main loop is done).
+// through the epilogue, one 32-row slice at a time. A lane's four columns
+// are the same in every row it visits, so its bias and gate are read once.
+// stage must hold 32 x (WN + 4) floats for each wave and be free (the main
+// loop is done).
 template <int TM, int TN, int WN>
 __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][TN],
                                                 float* stage, int row0, int col0) {
-  constexpr int CS = WN + 4;
-  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
-  const bool vec_ok = epilogue_vec_ok(a);
-#pragma unroll
-  for (int i = 0; i < TM; i++) {
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[i][j][r];
-    __syncthreads();
-    for (int it = lane; it < 32 * (WN / 4); it += 64) {
-      const int rl = it / (WN / 4), c4 = it % (WN / 4);
-      const float4 v = *(const float4*)&stage[rl * CS + c4 * 4];
-      epilogue_four(a, bidx, row0 + i * 32 + rl, col0 + c4 * 4, v, vec_ok);
-    }
-    __syncthreads();
-  }
+  constexpr int C4 = WN / 4;
+  const int lane = threadIdx.x & 63;
+  EpiLane L;
+  L.c4 = lane % C4;
+  L.rl0 = lane / C4;
+  L.col = col0 + L.c4 * 4;
+  L.n = min(4, a.N - L.col);
+  const int ep = a.epilogue;
+  const bool residual = ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL;
+  const bool act = ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU;
+  L.out_vec = aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype));
+  const bool res_vec = residual && aligned16(a.resid, a.ldr, a.batch_r, dtype_size(a.r_dtype));
+  // Uniform over the wave: all of its columns in range, aligned rows.
+  L.fast = !act && col0 + WN <= a.N && L.out_vec && (!residual || res_vec);
+  L.bias = make_float4(0.f, 0.f, 0.f, 0.f);
+  L.gate = make_float4(1.f, 1.f, 1.f, 1.f);
+  if (L.n > 0 && a.bias) L.bias = load_cols(a.bias, a.bias_dtype, L.col, L.n, (uintptr_t)a.bias % 16 == 0);
+  if (L.n > 0 && ep == EPI_GATED_RESIDUAL)
+    L.gate = load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + L.col, L.n,
+                       aligned16(a.gate, a.batch_gate, 0, dtype_size(a.gate_dtype)));
+  epilogue_slices<0, TM, TN, WN>(a, bidx, L, acc, stage, row0);
 }
 
 // Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile.
@@ -467,54 +555,66 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   issue_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  V af[2][TM], bf[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&As[0][swz(wm * WM + i * 32 + lrow, lhalf)];
+#pragma unroll
+  for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bs[0][swz(wn * WN + j * 32 + lrow, lhalf)];
+  constexpr int NF = TM + TN, NM = TM * TN, NS = BK / 16;
   for (int kt = 0; kt < KT; kt++) {
     const int cur = kt & 1;
-    // The tile after the last reads zeros (every offset is past K): the
-    // loop body stays one block for the scheduler.
+    // Tile kt + 1 goes into the other buffer, whose last reads (tile kt - 1)
+    // every wave finished before the previous iteration's barrier. The tile
+    // after the last reads zeros (every offset is past K): the loop body
+    // stays one block for the scheduler.
     issue_tile(kt + 1, cur ^ 1);
-    V af[2][TM], bf[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, lhalf)];
-#pragma unroll
-    for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bs[cur][swz(wn * WN + j * 32 + lrow, lhalf)];
-#pragma unroll
-    for (int s = 0; s < BK / 16; s++) {
+    for (int s = 0; s < NS; s++) {
       const int p = s & 1;
-      if (s + 1 < BK / 16) {
+      if (s + 1 < NS) {
         const int c = 2 * (s + 1) + lhalf;
 #pragma unroll
         for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, c)];
 #pragma unroll
         for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bs[cur][swz(wn * WN + j * 32 + lrow, c)];
+      } else {
+        // Before the last step's MFMAs: wait for this wave's part of tile
+        // kt + 1, meet the other waves (the whole tile has landed, and
+        // every read of tile kt is done), then read the next tile's first
+        // fragments under the last step's MFMAs. Waiting this late gives
+        // the DMA three of the four steps to land, and the next iteration
+        // starts with its fragments in registers.
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&As[cur ^ 1][swz(wm * WM + i * 32 + lrow, lhalf)];
+#pragma unroll
+        for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bs[cur ^ 1][swz(wn * WN + j * 32 + lrow, lhalf)];
       }
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[p][i], bf[p][j], acc[i][j]);
-    }
-    // Schedule: the tile DMA first, then the first step's fragments, then
-    // each step's MFMAs with the next step's LDS reads threaded between
-    // them (one read every TM*TN/(TM+TN) MFMAs).
-    constexpr int NF = TM + TN, NM = TM * TN;
-    __builtin_amdgcn_sched_group_barrier(0x0010, A_LOADS + B_LOADS, 0);
-    __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
-#pragma unroll
-    for (int s = 0; s < BK / 16 - 1; s++) {
+      // Schedule: the tile DMA first, then each step's MFMAs with the next
+      // fragments' LDS reads threaded between them.
+      if (s == 0) __builtin_amdgcn_sched_group_barrier(0x0010, A_LOADS + B_LOADS, 0);
       if (NM >= NF) {
 #pragma unroll
         for (int f = 0; f < NF; f++) {
           __builtin_amdgcn_sched_group_barrier(0x0008, NM / NF, 0);
           __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(0x0008, NM - (NM / NF) * NF, 0);
       } else {
         __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
         __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
       }
     }
-    __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
   staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
