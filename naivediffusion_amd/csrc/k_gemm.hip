@@ -283,8 +283,15 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx,
   epilogue_slices<0, TM, TN, WN>(a, bidx, L, acc, stage, row0);
 }
 
-// Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile.
-__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ (r & 7)) << 3); }
+// Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile
+// (128-byte rows). gfx950's LDS serves a ds_read_b128 sixteen lanes at a
+// time across 64 four-byte banks (256 bytes); the fragment reads have those
+// lanes on sixteen consecutive rows at one logical chunk, so the physical
+// chunk c ^ ((r / 2) % 8) puts them on sixteen distinct 16-byte bank
+// groups ((r % 2) * 8 + physical chunk). A plain c ^ (r % 8) would put rows
+// r and r + 8 on the same banks: a two-way conflict on every read.
+__device__ __forceinline__ int swz_key(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ swz_key(r)) << 3); }
 
 // Bounds-checked buffer loads: an offset at or past the resource's size
 // reads zeros, so the tile edges need no branches.
@@ -485,9 +492,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
            : make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * ES));
 
   // Lane l of a kilobyte load: row (l / 8) of its 8-row group, physical
-  // chunk l % 8 holding logical K chunk (l % 8) ^ (row % 8).
+  // chunk l % 8 holding logical K chunk (l % 8) ^ swz_key(row). Group q
+  // covers rows 8 q .. 8 q + 7, so swz_key(row) = 4 (q % 2) + (l / 8) / 2:
+  // the chunk depends on the group's parity.
   const int lrow8 = lane >> 3;
-  const int kchunk = (lane & 7) ^ lrow8;
+  const int kchunk_q[2] = {(lane & 7) ^ (lrow8 >> 1), (lane & 7) ^ (4 | (lrow8 >> 1))};
   uint32_t a_row[A_LOADS], w_row[B_LOADS];
   int pix_y[CONV ? B_LOADS : 1], pix_x[CONV ? B_LOADS : 1];
 #pragma unroll
@@ -511,12 +520,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   }
 
   auto issue_tile = [&](int kt, int buf) {
-    const int k = kt * BK + kchunk * 8;
-    const bool kin = k < a.K;
-    const uint32_t koff = uint32_t(k * ES);
+    int k[2];
+    bool kin[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      k[q] = kt * BK + kchunk_q[q] * 8;
+      kin[q] = k[q] < a.K;
+    }
 #pragma unroll
     for (int i = 0; i < A_LOADS; i++) {
-      const uint32_t off = (kin && a_row[i] != kOutOfRange) ? a_row[i] + koff : kOutOfRange;
+      const int q = (wave * A_LOADS + i) & 1;
+      const uint32_t off = (kin[q] && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k[q] * ES) : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
     }
     if (CONV) {
@@ -524,19 +538,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
       // and the channel offset are uniform over the workgroup.
       const int k0 = kt * BK;
       const int tap = k0 / a.conv_cin;
-      const int ci = k0 - tap * a.conv_cin + kchunk * 8;
+      const int ci0 = k0 - tap * a.conv_cin;
       const int ky = tap / a.conv_kw, kx = tap - ky * a.conv_kw;
 #pragma unroll
       for (int i = 0; i < B_LOADS; i++) {
+        const int q = (wave * B_LOADS + i) & 1;
         const int iy = pix_y[i] + ky, ix = pix_x[i] + kx;
-        const bool in = kin && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
-        const uint32_t off = in ? uint32_t(((iy * a.conv_w + ix) * a.conv_cin + ci) * ES) : kOutOfRange;
+        const bool in = kin[q] && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
+        const uint32_t off =
+            in ? uint32_t(((iy * a.conv_w + ix) * a.conv_cin + ci0 + kchunk_q[q] * 8) * ES) : kOutOfRange;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < B_LOADS; i++) {
-        const uint32_t off = (kin && w_row[i] != kOutOfRange) ? w_row[i] + koff : kOutOfRange;
+        const int q = (wave * B_LOADS + i) & 1;
+        const uint32_t off = (kin[q] && w_row[i] != kOutOfRange) ? w_row[i] + uint32_t(k[q] * ES) : kOutOfRange;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
       }
     }
@@ -660,9 +677,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * ES));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, (uint32_t)(int64_t(a.N - 1) * a.ldw + a.K));
 
-  // A: as the 16-bit kernel (8 rows x 8 swizzled 16-byte chunks per load).
+  // A: as the 16-bit kernel (8 rows x 8 swizzled 16-byte chunks per load,
+  // the chunk depending on the 8-row group's parity).
   const int lrow8 = lane >> 3;
-  const int kchunk = (lane & 7) ^ lrow8;
+  const int kchunk_q[2] = {(lane & 7) ^ (lrow8 >> 1), (lane & 7) ^ (4 | (lrow8 >> 1))};
   uint32_t a_row[A_LOADS], w_row[W_LOADS];
 #pragma unroll
   for (int i = 0; i < A_LOADS; i++) {
@@ -678,11 +696,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
   }
 
   auto issue_tile = [&](int kt, int buf) {
-    const int k = kt * BK + kchunk * 8;
-    const bool kin = k < a.K;
 #pragma unroll
     for (int i = 0; i < A_LOADS; i++) {
-      const uint32_t off = (kin && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k * ES) : kOutOfRange;
+      const int k = kt * BK + kchunk_q[(wave * A_LOADS + i) & 1] * 8;
+      const uint32_t off = (k < a.K && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k * ES) : kOutOfRange;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
     }
     const int kw = kt * BK + wchunk * 16;
@@ -1269,7 +1286,7 @@ void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
   const GemmArgs g = conv_gemm_args(c);
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   switch (conv_choose(g)) {
-    case CK_256: launch_mfma_lds<256, 256, 128, 64, true>(g, s); break;
+    case CK_256: launch_mfma_lds<256, 256, 64, 128, true>(g, s); break;
     case CK_128: launch_mfma_lds<128, 128, 64, 64, true>(g, s); break;
     case CK_64x128: launch_mfma_lds<64, 128, 32, 64, true>(g, s); break;
     default: launch_mfma_lds<64, 64, 32, 32, true>(g, s); break;
@@ -1317,7 +1334,7 @@ bool launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s, &b); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s, &b); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s, &b); break;
-    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s, &b); break;
+    case K_LDS_256W8: launch_mfma_lds<256, 256, 64, 128>(a, s, &b); break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s, &b); break;
     default: return false;
   }
@@ -1349,9 +1366,9 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
-    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s); break;
+    case K_LDS_256W8: launch_mfma_lds<256, 256, 64, 128>(a, s); break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
-    case K_W8_256W8: launch_w8_lds<256, 256, 128, 64>(a, s); break;
+    case K_W8_256W8: launch_w8_lds<256, 256, 64, 128>(a, s); break;
     case K_W8_128: launch_w8_lds<128, 128, 64, 64>(a, s); break;
     case K_W8_64x128: launch_w8_lds<64, 128, 32, 64>(a, s); break;
     case K_W8_64x64: launch_w8_lds<64, 64, 32, 32>(a, s); break;
