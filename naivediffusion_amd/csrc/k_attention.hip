@@ -70,18 +70,47 @@ __device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// LDS layouts of the key tile (64 rows of D elements) and the transposed
+// value tile (D rows of 64 keys), swizzled for gfx950's LDS: 64 four-byte
+// banks, a 16-byte read served sixteen lanes at a time and an 8-byte read
+// thirty-two at a time. The fragment reads put those lanes on consecutive
+// rows at one logical granule; the XOR keys below put them on distinct
+// banks. Keys: 16-byte chunk c of row `key`.
+template <int D>
+__device__ __forceinline__ int k_off(int key, int c) {
+  // D = 128: a row is 256 bytes, chunk c ^ (key % 16) is distinct over 16
+  // rows. D = 64: rows are 128 bytes, so rows r and r + 1 share the bank
+  // span; the key is (key / 2) % 8 together with the row's half.
+  const int x = D == 128 ? (key & 15) : ((key >> 1) & 7);
+  return key * D + ((c ^ x) << 3);
+}
+// Values: 8-byte group g (4 keys) of row d. Rows are 128 bytes; 32 lanes
+// read rows d .. d + 31, so the group is XORed with ((d / 2) ^ (d / 8)) % 16,
+// a bijection over the 16 rows of each parity; the writes (rows 8 i + 2 e
+// of sixteen lanes, see store_kv) are distinct under it too.
+__device__ __forceinline__ int vt_off(int d, int g) {
+  return d * 64 + ((g ^ (((d >> 1) ^ (d >> 3)) & 15)) << 2);
+}
+
 // One tile: 128 queries (4 waves x 32) of one (batch, head) over key blocks
 // [kb0, kb1) of 64 keys. With part == nullptr the tile covers every key and
 // writes the normalised output; otherwise it leaves its unnormalised O^T
 // registers, running max and partial row sum in `part` (field-major, one
 // float per thread per field) for attn_combine_kernel.
+//
+// Softmax: the running max is kept over raw scores, so a probability is one
+// fused multiply-add (score * scale * log2 e - max) and one v_exp_f32
+// (2^x; results below 2^-126 flush to zero, far below a bf16 probability's
+// resolution). Masks and the key tail change the raw scores in a uniform
+// branch (only the masked kernels and the last key block take it): a ruled-
+// out key gets -10000 / scale added, i.e. -10000 after scaling, and keys
+// past the end get -inf.
 template <typename T, int D, int MASK>
 __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int head, int b, int kb0, int kb1,
                                                float* part, T (*Ks)[64 * D], T (*Vt)[D * 64]) {
   typedef typename AMfma<T>::V V;
   constexpr int BQ = 128, BKEY = 64;
   constexpr int KCH = D / 8;                      // 16-byte chunks per key row
-  constexpr int KMASK = (KCH < 16 ? KCH : 16) - 1;
   constexpr int K_PER = BKEY * KCH / 256;         // K chunks per thread
   constexpr int V_TASKS = (BKEY / 4) * (D / 8);   // (4-key group, 8-d chunk) tasks
   constexpr int DT = D / 32;                      // output tiles along d
@@ -103,8 +132,41 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
   uint4 rk[K_PER];
   uint4 rv[4];
   const int vkg = tid / (D / 8), vdc = tid % (D / 8);
+  // Element offsets of this thread's K and V loads from the first row of a
+  // key block, for each of the two row segments (a joined sequence): a
+  // block inside one segment and inside the keys loads from one uniform
+  // base, one add per load.
+  // (Offsets fit in 32 bits when a row stride is below 2^24 elements.)
+  const bool small_ld = a.k.ld[0] < (1 << 24) && a.k.ld[1] < (1 << 24) && a.v.ld[0] < (1 << 24) &&
+                        a.v.ld[1] < (1 << 24);
+  int koff[2][K_PER], voff[2][4];
+#pragma unroll
+  for (int sg = 0; sg < 2; sg++) {
+    const uint32_t ld = (uint32_t)a.k.ld[sg], ldv = (uint32_t)a.v.ld[sg];
+#pragma unroll
+    for (int i = 0; i < K_PER; i++) {
+      const int id = tid + i * 256;
+      koff[sg][i] = (int)(uint32_t(id / KCH) * ld + uint32_t(col0) + uint32_t(id % KCH) * 8u);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) voff[sg][e] = (int)(uint32_t(vkg * 4 + e) * ldv + uint32_t(col0) + uint32_t(vdc) * 8u);
+  }
   auto load_kv = [&](int kb) {
     const int key0 = kb * BKEY;
+    const bool inside = small_ld && key0 + BKEY <= a.S && (key0 + BKEY <= a.k.rows0 || key0 >= a.k.rows0) &&
+                        (key0 + BKEY <= a.v.rows0 || key0 >= a.v.rows0);
+    if (inside) {
+      const int sk = key0 >= a.k.rows0, sv = key0 >= a.v.rows0;
+      const T* kbase = (const T*)a.k.ptr[sk] + b * a.k.batch[sk] + (key0 - sk * a.k.rows0) * a.k.ld[sk];
+      const T* vbase = (const T*)a.v.ptr[sv] + b * a.v.batch[sv] + (key0 - sv * a.v.rows0) * a.v.ld[sv];
+#pragma unroll
+      for (int i = 0; i < K_PER; i++) rk[i] = *(const uint4*)(kbase + (sk ? koff[1][i] : koff[0][i]));
+      if (tid < V_TASKS) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) rv[e] = *(const uint4*)(vbase + (sv ? voff[1][e] : voff[0][e]));
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < K_PER; i++) {
       const int id = tid + i * 256;
@@ -127,23 +189,26 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int i = 0; i < K_PER; i++) {
       const int id = tid + i * 256;
       const int key = id / KCH, c = id % KCH;
-      *(uint4*)&Ks[buf][key * D + ((c ^ (key & KMASK)) << 3)] = rk[i];
+      *(uint4*)&Ks[buf][k_off<D>(key, c)] = rk[i];
     }
     if (tid < V_TASKS) {
       const uint32_t w0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
       const uint32_t w1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
       const uint32_t w2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
       const uint32_t w3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
+      // Threads of odd key groups write their odd row first, so each write
+      // instruction covers both row parities (all 64 banks).
+      const int odd = vkg & 1;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         // Two d rows per 32-bit word: (d, d+1) of keys 4g..4g+3.
-        const uint32_t lo01 = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100);
-        const uint32_t lo23 = __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100);
-        const uint32_t hi01 = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302);
-        const uint32_t hi23 = __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302);
+        const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x05040100),
+                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100));
+        const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x07060302),
+                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302));
         const int d = vdc * 8 + 2 * e;
-        *(uint2*)&Vt[buf][d * BKEY + ((vkg ^ (d & 15)) << 2)] = make_uint2(lo01, lo23);
-        *(uint2*)&Vt[buf][(d + 1) * BKEY + ((vkg ^ ((d + 1) & 15)) << 2)] = make_uint2(hi01, hi23);
+        *(uint2*)&Vt[buf][vt_off(d + odd, vkg)] = odd ? hi : lo;
+        *(uint2*)&Vt[buf][vt_off(d + 1 - odd, vkg)] = odd ? lo : hi;
       }
     }
   };
@@ -155,8 +220,10 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int r = 0; r < 16; r++) o[j][r] = 0.f;
   float m_run = -INFINITY, l_part = 0.f;
   const float sl = a.scale * kLog2e;
-  const float mask_add = -10000.0f * kLog2e;
+  const bool pos = sl > 0.f;
+  const float mask_raw = -10000.0f / a.scale;
   const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
+  const f32x16 zero16 = {};
 
   load_kv(kb0);
   store_kv(0);
@@ -165,49 +232,56 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     const int cur = (kb - kb0) & 1;
     if (kb + 1 < kb1) load_kv(kb + 1);
 
-    // S^T for 64 keys: two 32-key tiles.
+    // S^T for 64 keys: two 32-key tiles (raw scores).
     f32x16 sacc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) sacc[kt][r] = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       const int key = kt * 32 + lq;
 #pragma unroll
       for (int s = 0; s < D / 16; s++) {
         const int c = 2 * s + lh;
-        const V kf = *(const V*)&Ks[cur][key * D + ((c ^ (key & KMASK)) << 3)];
-        sacc[kt] = AMfma<T>::mma(kf, qf[s], sacc[kt]);
+        const V kf = *(const V*)&Ks[cur][k_off<D>(key, c)];
+        sacc[kt] = AMfma<T>::mma(kf, qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     }
-    // Scale (into log2 units), mask, running max. The key tail is only
-    // checked in the last block.
-    const bool tail = (kb + 1) * BKEY > a.S;
-    float mloc = -INFINITY;
+    if (MASK != NDX_MASK_NONE || (kb + 1) * BKEY > a.S) {
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float x = sacc[kt][r] * sl;
-        const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (MASK == NDX_MASK_KEY_LENGTH) {
-          if (key >= key_len) x += mask_add;
-        } else if (MASK == NDX_MASK_BOOLEAN) {
-          const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
-                             int64_t(min(key, a.S - 1)) * a.mask_stride[3];
-          if (a.mask[mi] == 0) x += mask_add;
+        for (int r = 0; r < 16; r++) {
+          float x = sacc[kt][r];
+          const int key = kb * BKEY + kt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (MASK == NDX_MASK_KEY_LENGTH) {
+            if (key >= key_len) x += mask_raw;
+          } else if (MASK == NDX_MASK_BOOLEAN) {
+            const int64_t mi = b * a.mask_stride[0] + head * a.mask_stride[1] + int64_t(qm) * a.mask_stride[2] +
+                               int64_t(min(key, a.S - 1)) * a.mask_stride[3];
+            if (a.mask[mi] == 0) x += mask_raw;
+          }
+          if (key >= a.S) x = pos ? -INFINITY : INFINITY;
+          sacc[kt][r] = x;
         }
-        if (tail && key >= a.S) x = -INFINITY;
-        sacc[kt][r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
+    }
+    // Running max in scaled units: the largest raw score times a positive
+    // scale (the smallest for a negative one).
+    float mx = sacc[0][0];
+    if (pos) {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[kt][r]);
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mx = fminf(mx, sacc[kt][r]);
+    }
+    const float mloc = mx * sl;
+    const float m_new = fmaxf(m_run, fmaxf(mloc, __shfl_xor(mloc, 32, 64)));
     // Rescale the running output only when some lane's max moved: after
     // the first blocks the maxima settle and the multiply is skipped.
     if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_part *= alpha;
 #pragma unroll
       for (int j = 0; j < DT; j++)
@@ -219,7 +293,7 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float p = exp2f(sacc[kt][r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], sl, -m_new));
         sacc[kt][r] = p;
         l_part += p;
       }
@@ -233,9 +307,8 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) {
         const int d = dt * 32 + lq;
-        const int g1 = 4 * u + lh, g2 = 4 * u + 2 + lh;
-        const uint2 x1 = *(const uint2*)&Vt[cur][d * BKEY + ((g1 ^ (d & 15)) << 2)];
-        const uint2 x2 = *(const uint2*)&Vt[cur][d * BKEY + ((g2 ^ (d & 15)) << 2)];
+        const uint2 x1 = *(const uint2*)&Vt[cur][vt_off(d, 4 * u + lh)];
+        const uint2 x2 = *(const uint2*)&Vt[cur][vt_off(d, 4 * u + 2 + lh)];
         const V vf = __builtin_bit_cast(V, make_uint4(x1.x, x1.y, x2.x, x2.y));
         o[dt] = AMfma<T>::mma(vf, pb, o[dt]);
       }
