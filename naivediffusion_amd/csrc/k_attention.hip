@@ -87,7 +87,7 @@ __device__ __forceinline__ int k_off(int key, int c) {
 // Values: 8-byte group g (4 keys) of row d. Rows are 128 bytes; 32 lanes
 // read rows d .. d + 31, so the group is XORed with ((d / 2) ^ (d / 8)) % 16,
 // a bijection over the 16 rows of each parity; the writes (rows 8 i + 2 e
-// of sixteen lanes, see store_kv) are distinct under it too.
+// of sixteen lanes, see store_v) are distinct under it too.
 __device__ __forceinline__ int vt_off(int d, int g) {
   return d * 64 + ((g ^ (((d >> 1) ^ (d >> 3)) & 15)) << 2);
 }
@@ -107,11 +107,11 @@ __device__ __forceinline__ int vt_off(int d, int g) {
 // past the end get -inf.
 template <typename T, int D, int MASK>
 __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int head, int b, int kb0, int kb1,
-                                               float* part, T (*Ks)[64 * D], T (*Vt)[D * 64]) {
+                                               float* part, T (*__restrict__ Ks)[64 * D],
+                                               T (*__restrict__ Vt)[D * 64]) {
   typedef typename AMfma<T>::V V;
   constexpr int BQ = 128, BKEY = 64;
   constexpr int KCH = D / 8;                      // 16-byte chunks per key row
-  constexpr int K_PER = BKEY * KCH / 256;         // K chunks per thread
   constexpr int V_TASKS = (BKEY / 4) * (D / 8);   // (4-key group, 8-d chunk) tasks
   constexpr int DT = D / 32;                      // output tiles along d
 
@@ -129,69 +129,84 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int s = 0; s < D / 16; s++) qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
   }
 
-  uint4 rk[K_PER];
+  // K goes global -> LDS by DMA (buffer_load ... lds): a wave-wide load
+  // fills one kilobyte, KROWS rows; lane l lands at byte 16 l (row l / (D/8)
+  // of the group, physical chunk l % (D/8)) and fetches the logical chunk
+  // that k_off places there. V goes through registers (it is transposed on
+  // its way into LDS).
+  constexpr int KROWS = 512 / D;            // key rows per kilobyte load
+  constexpr int K_LOADS = BKEY / KROWS / 4; // loads per wave per block
+  const int kr = lane / (D / 8), kpc = lane % (D / 8);
+  int kcol[K_LOADS];
+#pragma unroll
+  for (int i = 0; i < K_LOADS; i++) {
+    const int key = (wave * K_LOADS + i) * KROWS + kr;
+    const int x = D == 128 ? (key & 15) : ((key >> 1) & 7);
+    kcol[i] = (int)col0 + ((kpc ^ x) << 3);
+  }
   uint4 rv[4];
   const int vkg = tid / (D / 8), vdc = tid % (D / 8);
-  // Element offsets of this thread's K and V loads from the first row of a
-  // key block, for each of the two row segments (a joined sequence): a
-  // block inside one segment and inside the keys loads from one uniform
-  // base, one add per load.
   // (Offsets fit in 32 bits when a row stride is below 2^24 elements.)
   const bool small_ld = a.k.ld[0] < (1 << 24) && a.k.ld[1] < (1 << 24) && a.v.ld[0] < (1 << 24) &&
                         a.v.ld[1] < (1 << 24);
-  int koff[2][K_PER], voff[2][4];
-#pragma unroll
-  for (int sg = 0; sg < 2; sg++) {
-    const uint32_t ld = (uint32_t)a.k.ld[sg], ldv = (uint32_t)a.v.ld[sg];
-#pragma unroll
-    for (int i = 0; i < K_PER; i++) {
-      const int id = tid + i * 256;
-      koff[sg][i] = (int)(uint32_t(id / KCH) * ld + uint32_t(col0) + uint32_t(id % KCH) * 8u);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) voff[sg][e] = (int)(uint32_t(vkg * 4 + e) * ldv + uint32_t(col0) + uint32_t(vdc) * 8u);
-  }
-  auto load_kv = [&](int kb) {
+  // The base of key block kb in segment sg of s: blocks inside one segment
+  // (and the whole block below S, for V) take one uniform base. Ternaries,
+  // not s.ptr[sg]: a runtime index into the kernel arguments makes the
+  // compiler fetch them from memory on every block.
+  auto seg_base = [&](const AttnSeg& sgm, int key0, bool second) -> const T* {
+    return second ? (const T*)sgm.ptr[1] + b * sgm.batch[1] + (key0 - sgm.rows0) * sgm.ld[1]
+                  : (const T*)sgm.ptr[0] + b * sgm.batch[0] + key0 * sgm.ld[0];
+  };
+  auto issue_k = [&](int kb, int buf) {
     const int key0 = kb * BKEY;
-    const bool inside = small_ld && key0 + BKEY <= a.S && (key0 + BKEY <= a.k.rows0 || key0 >= a.k.rows0) &&
-                        (key0 + BKEY <= a.v.rows0 || key0 >= a.v.rows0);
-    if (inside) {
-      const int sk = key0 >= a.k.rows0, sv = key0 >= a.v.rows0;
-      const T* kbase = (const T*)a.k.ptr[sk] + b * a.k.batch[sk] + (key0 - sk * a.k.rows0) * a.k.ld[sk];
-      const T* vbase = (const T*)a.v.ptr[sv] + b * a.v.batch[sv] + (key0 - sv * a.v.rows0) * a.v.ld[sv];
+    const bool second = key0 >= a.k.rows0;
+    if (small_ld && (second || key0 + BKEY <= a.k.rows0)) {
+      // Rows past the keys (or past the segment) read as zeros.
+      const int64_t end = second ? a.S : std::min<int64_t>(a.k.rows0, a.S);
+      const int rows = (int)std::min<int64_t>(BKEY, end - key0);
+      const int64_t ld = second ? a.k.ld[1] : a.k.ld[0];
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(seg_base(a.k, key0, second), uint32_t(rows * ld * 2));
 #pragma unroll
-      for (int i = 0; i < K_PER; i++) rk[i] = *(const uint4*)(kbase + (sk ? koff[1][i] : koff[0][i]));
-      if (tid < V_TASKS) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) rv[e] = *(const uint4*)(vbase + (sv ? voff[1][e] : voff[0][e]));
+      for (int i = 0; i < K_LOADS; i++) {
+        const int key = (wave * K_LOADS + i) * KROWS + kr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&Ks[buf][(wave * K_LOADS + i) * KROWS * D], 16,
+                                                 uint32_t((key * ld + kcol[i]) * 2), 0, 0, 0);
       }
       return;
     }
-#pragma unroll
-    for (int i = 0; i < K_PER; i++) {
+    // A block across the two segments (or huge strides): chunk by chunk
+    // through registers.
+#pragma unroll 1
+    for (int i = 0; i < BKEY * KCH / 256; i++) {
       const int id = tid + i * 256;
       const int key = id / KCH, c = id % KCH;
       const int gk = min(key0 + key, a.S - 1);  // tail keys are masked below
-      rk[i] = *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8);
-    }
-    if (tid < V_TASKS) {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int gk = key0 + vkg * 4 + e;
-        // Tail rows must be zero: a zero probability times a stale value
-        // could still be NaN.
-        rv[e] = gk < a.S ? *(const uint4*)(seg_row<T>(a.v, b, gk) + col0 + vdc * 8) : make_uint4(0, 0, 0, 0);
-      }
+      *(uint4*)&Ks[buf][k_off<D>(key, c)] = *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8);
     }
   };
-  auto store_kv = [&](int buf) {
+  // V rows through registers, branch free (a branch here would make the
+  // compiler copy the loaded registers at the join, waiting for the loads):
+  // the row is clamped into the keys and its segment picked by selects;
+  // rows past the keys are zeroed when stored.
+  const int64_t v_ld0 = a.v.ld[0], v_ld1 = a.v.ld[1];
+  const T* v_base0 = (const T*)a.v.ptr[0] + b * a.v.batch[0] + col0 + vdc * 8;
+  const T* v_base1 = (const T*)a.v.ptr[1] + b * a.v.batch[1] - a.v.rows0 * a.v.ld[1] + col0 + vdc * 8;
+  auto load_v = [&](int kb) {
+    if (tid >= V_TASKS) return;
 #pragma unroll
-    for (int i = 0; i < K_PER; i++) {
-      const int id = tid + i * 256;
-      const int key = id / KCH, c = id % KCH;
-      *(uint4*)&Ks[buf][k_off<D>(key, c)] = rk[i];
+    for (int e = 0; e < 4; e++) {
+      const int gk = min(kb * BKEY + vkg * 4 + e, a.S - 1);
+      const T* p = gk < a.v.rows0 ? v_base0 + gk * v_ld0 : v_base1 + gk * v_ld1;
+      rv[e] = *(const uint4*)p;
     }
+  };
+  auto store_v = [&](int buf, int kb) {
     if (tid < V_TASKS) {
+      // Tail rows must be zero: a zero probability times a stale value
+      // could still be NaN.
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (kb * BKEY + vkg * 4 + e >= a.S) rv[e] = make_uint4(0, 0, 0, 0);
       const uint32_t w0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
       const uint32_t w1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
       const uint32_t w2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
@@ -225,12 +240,19 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
   const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
   const f32x16 zero16 = {};
 
-  load_kv(kb0);
-  store_kv(0);
+  issue_k(kb0, 0);
+  load_v(kb0);
+  store_v(0, kb0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int kb = kb0; kb < kb1; kb++) {
     const int cur = (kb - kb0) & 1;
-    if (kb + 1 < kb1) load_kv(kb + 1);
+    // Block kb + 1 goes into the other buffers, whose last reads (block
+    // kb - 1) every wave finished before the previous barrier: V into
+    // registers now, K by DMA once this block's key fragments are read (an
+    // LDS read after a DMA into the same array waits for the DMA; Ks and Vt
+    // are distinct restrict pointers, so the value reads below do not).
+    if (kb + 1 < kb1) load_v(kb + 1);
 
     // S^T for 64 keys: two 32-key tiles (raw scores).
     f32x16 sacc[2];
@@ -244,6 +266,7 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
         sacc[kt] = AMfma<T>::mma(kf, qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     }
+    if (kb + 1 < kb1) issue_k(kb + 1, cur ^ 1);
     if (MASK != NDX_MASK_NONE || (kb + 1) * BKEY > a.S) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
@@ -313,7 +336,10 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
         o[dt] = AMfma<T>::mma(vf, pb, o[dt]);
       }
     }
-    if (kb + 1 < kb1) store_kv(cur ^ 1);
+    if (kb + 1 < kb1) store_v(cur ^ 1, kb + 1);
+    // This wave's DMA of block kb + 1 has landed; after the barrier, every
+    // wave's has.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 

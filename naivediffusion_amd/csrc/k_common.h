@@ -14,6 +14,18 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Bounds-checked buffer loads: an offset at or past the resource's size
+// reads zeros (a load straight to LDS writes zeros), so tile edges need no
+// branches.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // Word 3 = 0x00020000: raw 32-bit dword access, the gfx9-family setting.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+// An LDS address for buffer_load ... lds (wave-uniform; lane l lands at
+// byte 16 l of a 16-byte-per-lane load).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
   return __uint_as_float(uint32_t(h) << 16);
 }

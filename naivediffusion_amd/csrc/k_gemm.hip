@@ -293,13 +293,6 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx,
 __device__ __forceinline__ int swz_key(int r) { return (r >> 1) & 7; }
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ swz_key(r)) << 3); }
 
-// Bounds-checked buffer loads: an offset at or past the resource's size
-// reads zeros, so the tile edges need no branches.
-constexpr uint32_t kOutOfRange = 0x80000000u;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  // Word 3 = 0x00020000: raw 32-bit dword access, the gfx9-family setting.
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
-}
 __device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
@@ -453,7 +446,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 // or LDS-write instruction is spent on staging. Fragments are double
 // buffered in registers: the LDS reads of step s + 1 are in flight while
 // the MFMAs of step s run.
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // a0 and a1 are two products with the same N, K and batch run as one grid
 // (a0's row tiles first, then a1's); a1.M = 0 for a single product.
