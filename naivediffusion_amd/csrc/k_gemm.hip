@@ -978,37 +978,106 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
 
 // M <= 4 rows: the rows go to LDS as fp32, each wave produces 4 output
 // features, lanes stride K in runs of 8 so every weight load is 16 bytes.
-template <int MR>
+// Eight weights of row n from column k (k a multiple of 8) widened to fp32,
+// the weight type fixed at compile time so the loads of several rows and
+// K steps can be in flight together.
+template <int WT, bool SF16 = true>
+__device__ __forceinline__ void load_w8_t(const GemmArgs& a, const char* W, int n, int k, float (&out)[8]) {
+  if constexpr (WT == NDX_F32) {
+    const float4* p = (const float4*)(W + (int64_t(n) * a.ldw + k) * 4);
+    const float4 x = p[0], y = p[1];
+    out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+    out[4] = y.x; out[5] = y.y; out[6] = y.z; out[7] = y.w;
+  } else if constexpr (WT == NDX_BF16) {
+    const uint4 v = *(const uint4*)(W + (int64_t(n) * a.ldw + k) * 2);
+    const uint16_t* h = (const uint16_t*)&v;
+#pragma unroll
+    for (int e = 0; e < 8; e++) out[e] = bf16_bits_to_f32(h[e]);
+  } else if constexpr (WT == NDX_F16) {
+    const uint4 v = *(const uint4*)(W + (int64_t(n) * a.ldw + k) * 2);
+    const _Float16* h = (const _Float16*)&v;
+#pragma unroll
+    for (int e = 0; e < 8; e++) out[e] = (float)h[e];
+  } else {  // int8, one scale (fp16 or fp32 by SF16) per qblock columns (a multiple of 8)
+    const uint2 v = *(const uint2*)(W + int64_t(n) * a.ldw + k);
+    const int8_t* q = (const int8_t*)&v;
+    const int64_t si = int64_t(n) * a.lds + k / a.qblock;
+    const float sc = SF16 ? (float)((const _Float16*)a.scales)[si] : ((const float*)a.scales)[si];
+#pragma unroll
+    for (int e = 0; e < 8; e++) out[e] = float(q[e]) * sc;
+  }
+}
+
+// A handful of rows (MR <= 4) times the weight: x goes to LDS once per
+// workgroup (fp32), then each wave takes four output features at once, its
+// lanes striding K by 8 columns, so every iteration has four 16-byte weight
+// loads per lane in flight (two iterations unrolled: eight); the weight
+// bytes are the whole cost.
+template <int MR, int WT, bool SF16 = true>
 __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs a) {
   extern __shared__ float xs[];  // [MR][K]
   const int64_t bidx = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < MR * a.K; i += 256) {
-    int m = i / a.K, k = i % a.K;
-    xs[i] = m < a.M ? load_f(a.a, a.a_dtype, bidx * a.batch_a + int64_t(m) * a.lda + k) : 0.f;
+  const int K = a.K;
+  if (a.a_dtype == NDX_F32 && K % 4 == 0 && a.lda % 4 == 0 && a.batch_a % 4 == 0 && (uintptr_t)a.a % 16 == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const float* xr = (const float*)a.a + bidx * a.batch_a + int64_t(min(m, a.M - 1)) * a.lda;
+      // Four loads out before the first store.
+      for (int k0 = 0; k0 < K; k0 += 4096) {
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int k = k0 + j * 1024 + tid * 4;
+          v[j] = k < K ? *(const float4*)(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int k = k0 + j * 1024 + tid * 4;
+          if (k < K) *(float4*)&xs[m * K + k] = m < a.M ? v[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < MR * K; i += 256) {
+      const int m = i / K, k = i % K;
+      xs[i] = m < a.M ? load_f(a.a, a.a_dtype, bidx * a.batch_a + int64_t(m) * a.lda + k) : 0.f;
+    }
   }
   __syncthreads();
   const char* W = (const char*)a.w;
   const int nbase = blockIdx.x * 16 + wave * 4;
+  int rows[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) rows[q] = min(nbase + q, a.N - 1);  // rows past N load row N-1, unused
+  float acc[4][MR];
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[q][m] = 0.f;
+#pragma unroll 2
+  for (int k = lane * 8; k < K; k += 512) {
+    float w[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) load_w8_t<WT, SF16>(a, W, rows[q], k, w[q]);
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float xv[8];
+      const float4 x0 = *(const float4*)&xs[m * K + k], x1 = *(const float4*)&xs[m * K + k + 4];
+      xv[0] = x0.x; xv[1] = x0.y; xv[2] = x0.z; xv[3] = x0.w; xv[4] = x1.x; xv[5] = x1.y; xv[6] = x1.z; xv[7] = x1.w;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[q][m] += xv[e] * w[q][e];
+    }
+  }
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int n = nbase + q;
-    if (n >= a.N) break;
-    float acc[MR];
-#pragma unroll
-    for (int m = 0; m < MR; m++) acc[m] = 0.f;
-    for (int k = lane * 8; k < a.K; k += 512) {
-      float w[8];
-      load_w8(a, W, n, k, w);
-#pragma unroll
-      for (int m = 0; m < MR; m++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[m] += xs[m * a.K + k + e] * w[e];
-    }
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-      float v = wave_sum(acc[m]);
-      if (lane == 0 && m < a.M) {
+      const float v = wave_sum(acc[q][m]);
+      if (lane == 0 && m < a.M && n < a.N) {
         const float bias = a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f;
         const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + n) : 0.f;
         epilogue_one(a, bidx, m, n, v, bias, gate);
@@ -1345,9 +1414,18 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_GEMV: {
       dim3 g((a.N + 15) / 16, a.batch);
       size_t lds = size_t(4) * a.K * sizeof(float);
-      if (a.M == 1) hipLaunchKernelGGL(gemv_kernel<1>, g, dim3(256), lds / 4, s, a);
-      else if (a.M == 2) hipLaunchKernelGGL(gemv_kernel<2>, g, dim3(256), lds / 2, s, a);
-      else hipLaunchKernelGGL(gemv_kernel<4>, g, dim3(256), lds, s, a);
+#define NDX_GEMV(MR, BYTES)                                                                         \
+  do {                                                                                              \
+    if (a.w_dtype == NDX_BF16) hipLaunchKernelGGL((gemv_kernel<MR, NDX_BF16>), g, dim3(256), BYTES, s, a); \
+    else if (a.w_dtype == NDX_F16) hipLaunchKernelGGL((gemv_kernel<MR, NDX_F16>), g, dim3(256), BYTES, s, a); \
+    else if (a.w_dtype == NDX_F32) hipLaunchKernelGGL((gemv_kernel<MR, NDX_F32>), g, dim3(256), BYTES, s, a); \
+    else if (a.s_dtype == NDX_F16) hipLaunchKernelGGL((gemv_kernel<MR, NDX_I8, true>), g, dim3(256), BYTES, s, a); \
+    else hipLaunchKernelGGL((gemv_kernel<MR, NDX_I8, false>), g, dim3(256), BYTES, s, a);        \
+  } while (0)
+      if (a.M == 1) NDX_GEMV(1, lds / 4);
+      else if (a.M == 2) NDX_GEMV(2, lds / 2);
+      else NDX_GEMV(4, lds);
+#undef NDX_GEMV
       break;
     }
     case K_MFMA_256: launch_mfma<256, 256, 128, 128>(a, s); break;
