@@ -240,6 +240,22 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
   const int key_len = MASK == NDX_MASK_KEY_LENGTH ? a.mask[0] : a.S;
   const f32x16 zero16 = {};
 
+  // Byte offsets of this lane's fragment reads within one buffer. Keys:
+  // step s reads chunk 2 s + lh of row lq (the second 32-key tile is 32 rows
+  // on); the swizzle key of row kt * 32 + lq does not depend on kt. Values:
+  // d = dt * 32 + lq and group g = 4 u + 2 p + lh; the swizzle key of row d
+  // is that of row lq with bit 2 flipped by dt, so the read offset depends on
+  // (u ^ dt, p) and dt only adds 32 rows.
+  constexpr int NSD = D / 16;
+  int kq[NSD], vq[8];
+  {
+    const int kx = D == 128 ? (lq & 15) : ((lq >> 1) & 7);
+#pragma unroll
+    for (int s2 = 0; s2 < NSD; s2++) kq[s2] = (lq * D + (((2 * s2 + lh) ^ kx) << 3)) * 2;
+    const int vx = ((lq >> 1) ^ (lq >> 3)) & 15;
+#pragma unroll
+    for (int w = 0; w < 8; w++) vq[w] = (lq * 64 + ((((w >> 1) << 2) | ((w & 1) << 1) | lh) ^ vx) * 4) * 2;
+  }
   issue_k(kb0, 0);
   load_v(kb0);
   store_v(0, kb0);
@@ -254,16 +270,19 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     // are distinct restrict pointers, so the value reads below do not).
     if (kb + 1 < kb1) load_v(kb + 1);
 
-    // S^T for 64 keys: two 32-key tiles (raw scores).
+    // S^T for 64 keys: two 32-key tiles (raw scores), the key fragment of
+    // the next step read under the current step's MFMA.
     f32x16 sacc[2];
+    {
+      const char* kbuf = (const char*)Ks[cur];
+      V kf[2];
+      kf[0] = *(const V*)(kbuf + kq[0]);
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      const int key = kt * 32 + lq;
-#pragma unroll
-      for (int s = 0; s < D / 16; s++) {
-        const int c = 2 * s + lh;
-        const V kf = *(const V*)&Ks[cur][k_off<D>(key, c)];
-        sacc[kt] = AMfma<T>::mma(kf, qf[s], s == 0 ? zero16 : sacc[kt]);
+      for (int i = 0; i < 2 * NSD; i++) {
+        const int kt = i / NSD, s = i % NSD;
+        if (i + 1 < 2 * NSD)
+          kf[(i + 1) & 1] = *(const V*)(kbuf + kq[(i + 1) % NSD] + ((i + 1) / NSD) * (32 * D * 2));
+        sacc[kt] = AMfma<T>::mma(kf[i & 1], qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     }
     if (kb + 1 < kb1) issue_k(kb + 1, cur ^ 1);
@@ -329,9 +348,9 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
       for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) {
-        const int d = dt * 32 + lq;
-        const uint2 x1 = *(const uint2*)&Vt[cur][vt_off(d, 4 * u + lh)];
-        const uint2 x2 = *(const uint2*)&Vt[cur][vt_off(d, 4 * u + 2 + lh)];
+        const char* vrow = (const char*)Vt[cur] + dt * 4096;
+        const uint2 x1 = *(const uint2*)(vrow + vq[((u ^ dt) << 1) | 0]);
+        const uint2 x2 = *(const uint2*)(vrow + vq[((u ^ dt) << 1) | 1]);
         const V vf = __builtin_bit_cast(V, make_uint4(x1.x, x1.y, x2.x, x2.y));
         o[dt] = AMfma<T>::mma(vf, pb, o[dt]);
       }
