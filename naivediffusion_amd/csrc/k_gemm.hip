@@ -449,7 +449,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
 // a0 and a1 are two products with the same N, K and batch run as one grid
 // (a0's row tiles first, then a1's); a1.M = 0 for a single product.
-template <int BM, int BN, int WM, int WN, typename T, bool CONV>
+template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
                                                                                     int grid) {
   typedef typename MfmaOp<T>::V V;
@@ -473,7 +473,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   if (second) tm -= tiles_m0;
   const int64_t bidx = blockIdx.y;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform: from an SGPR, every LDS destination of the
+  // tile DMA is scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   constexpr int ES = (int)sizeof(T);
 
@@ -511,6 +513,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
     }
   }
 
+  // With K a multiple of BK (KFULL) no tile reaches past K except the one
+  // loaded after the last (never read): no per-load K check. A row past M
+  // keeps kOutOfRange plus any K offset, still past the buffer's end.
   auto issue_tile = [&](int kt, int buf) {
     int k[2];
     bool kin[2];
@@ -519,13 +524,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
       k[q] = kt * BK + kchunk_q[q] * 8;
       kin[q] = k[q] < a.K;
     }
+    if constexpr (KFULL) {
 #pragma unroll
-    for (int i = 0; i < A_LOADS; i++) {
-      const int q = (wave * A_LOADS + i) & 1;
-      const uint32_t off = (kin[q] && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k[q] * ES) : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      for (int i = 0; i < A_LOADS; i++) {
+        const int q = (wave * A_LOADS + i) & 1;
+        const uint32_t off = a_row[i] + uint32_t(k[q] * ES);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < A_LOADS; i++) {
+        const int q = (wave * A_LOADS + i) & 1;
+        const uint32_t off = (kin[q] && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k[q] * ES) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      }
     }
-    if (CONV) {
+    if constexpr (CONV) {
       // A K tile lies within one tap (Cin is a multiple of BK): (ky, kx)
       // and the channel offset are uniform over the workgroup.
       const int k0 = kt * BK;
@@ -539,6 +553,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
         const bool in = kin[q] && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
         const uint32_t off =
             in ? uint32_t(((iy * a.conv_w + ix) * a.conv_cin + ci0 + kchunk_q[q] * 8) * ES) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      }
+    } else if constexpr (KFULL) {
+#pragma unroll
+      for (int i = 0; i < B_LOADS; i++) {
+        const int q = (wave * B_LOADS + i) & 1;
+        const uint32_t off = w_row[i] + uint32_t(k[q] * ES);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
       }
     } else {
@@ -1286,10 +1307,22 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
   int tiles = ((a.M + BM - 1) / BM + (a1.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   int grid = (tiles + 7) / 8 * 8;
   dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
-  if (a.a_dtype == NDX_BF16)
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, CONV>), g, b, 0, s, a, a1, grid);
-  else
-    hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, CONV>), g, b, 0, s, a, a1, grid);
+  // A convolution's K (taps x Cin, Cin a multiple of BK) is always whole.
+  if constexpr (CONV) {
+    if (a.a_dtype == NDX_BF16)
+      hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, true, true>), g, b, 0, s, a, a1, grid);
+    else
+      hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, true, true>), g, b, 0, s, a, a1, grid);
+  } else {
+    const bool kfull = a.K % BK == 0;
+    if (a.a_dtype == NDX_BF16) {
+      if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true>), g, b, 0, s, a, a1, grid);
+      else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, false>), g, b, 0, s, a, a1, grid);
+    } else {
+      if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true>), g, b, 0, s, a, a1, grid);
+      else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, false>), g, b, 0, s, a, a1, grid);
+    }
+  }
 }
 
 // ---- implicit-GEMM convolution ----------------------------------------------
