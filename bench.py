@@ -4,9 +4,11 @@ MI355X, bf16 compute (or int8 block-quantised weights with --int8), inputs
 resident in HBM before the timed region.
 
 Prints one JSON line: s/step, the roofline of the dominant kernel (algorithmic
-flops per launch over its HIP-event-timed average launch), and the CPU
-baseline (the oracle's restatement of the reference's C# CPU layer path,
-timed on this host over one block of the same step and scaled to 60 blocks).
+flops per launch over its average launch, timed by HIP events around its
+launches inside the timed steps), and the CPU baseline (the oracle's
+restatement of the reference's C# CPU layer path, timed on this host over one
+block of the same step and scaled to 60 blocks). The per-family breakdown
+comes from one untimed step with every kernel bracketed.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--compute bf16|f32|f16] [--no-cpu-baseline]
     python bench.py --workload anima|sdxl   # the Anima DiT / SDXL UNet steps (their own lines)
@@ -123,37 +125,54 @@ def cpu_baseline(device, cfg, seed, ni, nt):
     }
 
 
+def is_mfma_family(name):
+    return (name.startswith("gemm_") and "generic" not in name) or name.startswith("conv_mfma") or \
+        name.startswith("attention")
+
+
 def measure(dev, compiled, inputs, out, steps, warmup):
-    """W untimed steps, then K timed steps with every kernel bracketed by
-    HIP events on the device's stream (the stream all kernels run on)."""
+    """W untimed steps; one untimed step with every kernel bracketed by HIP
+    events (the per-family breakdown, and which MFMA family dominates); then
+    K timed steps in which only that family's launches are bracketed, on the
+    stream each is launched on, with nothing waiting between steps: the
+    step time carries a few events per step instead of two per kernel and a
+    wait per step. Returns (seconds per timed step, breakdown of the profiled
+    step, the dominant family's events over the timed steps)."""
     for _ in range(warmup):
         compiled.DispatchInto(inputs, out)
     dev.Synchronize()
     log(f"warmup done ({warmup} steps)")
     compiled.SetProfiling(True)
+    compiled.DispatchInto(inputs, out)
+    breakdown = compiled.Profile()
+    compiled.SetProfiling(False)
+    dominant = max((k for k in breakdown if is_mfma_family(k)), key=lambda k: breakdown[k]["ms"])
+    compiled.SetProfiling(True, family=dominant)
     dev.Synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         compiled.DispatchInto(inputs, out)
     dev.Synchronize()
     elapsed = time.perf_counter() - t0
-    prof = compiled.Profile()
+    timed = compiled.Profile()
     compiled.SetProfiling(False)
     log(f"{steps} steps in {elapsed:.3f} s: {elapsed / steps * 1e3:.1f} ms/step")
-    for name, e in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+    log("kernel families (one untimed step, every kernel bracketed):")
+    for name, e in sorted(breakdown.items(), key=lambda kv: -kv[1]["ms"]):
         tf = e["flops"] / (e["ms"] * 1e-3) / 1e12 if e["ms"] else 0.0
         gbs = e["bytes"] / (e["ms"] * 1e-3) / 1e9 if e["ms"] else 0.0
-        log(f"  {name:28s} {e['launches'] // steps:5d}/step {e['ms'] / steps:9.2f} ms/step "
-            f"{tf:8.1f} TFLOP/s {gbs:8.1f} GB/s")
-    return elapsed / steps, prof
+        log(f"  {name:28s} {e['launches']:5d}/step {e['ms']:9.2f} ms/step {tf:8.1f} TFLOP/s {gbs:8.1f} GB/s")
+    d = timed[dominant]
+    log(f"timed steps, {dominant}: {d['launches'] // steps}/step {d['ms'] / steps:.2f} ms/step "
+        f"{d['flops'] / (d['ms'] * 1e-3) / 1e12:.1f} TFLOP/s")
+    return elapsed / steps, breakdown, (dominant, d)
 
 
-def roofline(prof, steps, peak, workload):
+def roofline(dominant, steps, peak, workload):
     """The dominant MFMA kernel family (GEMM, convolution or attention) by
-    time: algorithmic flops per launch over its event-timed average launch."""
-    mfma = {k: v for k, v in prof.items()
-            if (k.startswith("gemm_") and "generic" not in k) or k.startswith("conv_mfma") or k.startswith("attention")}
-    name, dom = max(mfma.items(), key=lambda kv: kv[1]["ms"])
+    time: algorithmic flops per launch over its average launch, both from the
+    events bracketing its launches in the timed steps."""
+    name, dom = dominant
     per_launch = dom["flops"] / dom["launches"]
     avg_ms = dom["ms"] / dom["launches"]
     achieved = per_launch / (avg_ms * 1e-3) / 1e12
@@ -326,10 +345,10 @@ def main():
     log(f"graph built and compiled in {time.perf_counter() - t0:.1f} s: {compiled.KernelCount} kernels/step, "
         f"{compiled.PersistentSize / 1e9:.1f} GB weights, {compiled.TemporarySize / 1e9:.2f} GB scratch")
 
-    s_per_step, prof = measure(dev, compiled, setup["inputs"], setup["out"], args.steps, args.warmup)
+    s_per_step, prof, dominant = measure(dev, compiled, setup["inputs"], setup["out"], args.steps, args.warmup)
     peak = FP32_PEAK_TFLOPS if args.compute == "f32" else MFMA_BF16_PEAK_TFLOPS
-    total_flops = sum(e["flops"] for e in prof.values()) / args.steps
-    kernel_ms = sum(e["ms"] for e in prof.values()) / args.steps
+    total_flops = sum(e["flops"] for e in prof.values())
+    kernel_ms = sum(e["ms"] for e in prof.values())
 
     cpu = None
     if not args.no_cpu_baseline and setup["cpu"] is not None:
@@ -360,8 +379,10 @@ def main():
         "dtype": args.compute,
         "data": setup["data"],
         "config": config,
-        "roofline": roofline(prof, args.steps, peak, args.workload),
-        "kernels": {k: {"ms_per_step": v["ms"] / args.steps, "launches_per_step": v["launches"] // args.steps,
+        "roofline": roofline(dominant, args.steps, peak, args.workload),
+        # From one untimed step with every kernel bracketed (two events per
+        # kernel and a wait: the breakdown, not the timed step).
+        "kernels": {k: {"ms_per_step": v["ms"], "launches_per_step": v["launches"],
                         "tflops": (v["flops"] / (v["ms"] * 1e-3) / 1e12) if v["ms"] else 0.0,
                         "gbs": (v["bytes"] / (v["ms"] * 1e-3) / 1e9) if v["ms"] else 0.0}
                     for k, v in prof.items()},

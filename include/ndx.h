@@ -323,6 +323,12 @@ NDX_API ndx_status ndx_model_run_into_async(ndx_model* model, ndx_tensor* const*
 /* Kernel timing with no reference counterpart: while enabled, every kernel a
  * run launches is bracketed by HIP events on the device stream. */
 NDX_API ndx_status ndx_model_set_profiling(ndx_model* model, int32_t enabled);
+/* No counterpart in the reference either: with a family name (as the
+ * profile entries name them), profiling brackets only that family's kernels
+ * and waits for nothing until the entries are read, so a timed run carries
+ * a few events instead of two per kernel and a wait per run. NULL or ""
+ * returns to bracketing every kernel. */
+NDX_API ndx_status ndx_model_set_profile_filter(ndx_model* model, const char* family);
 /* Per kernel family since profiling was enabled: the family name, launches,
  * summed milliseconds and summed algorithmic flops and bytes. index runs
  * 0..families-1; returns NDX_INVALID_ARG past the end. */

@@ -184,6 +184,13 @@ struct ndx_model {
   int kernels = 0;
   bool profiling = false;
   std::vector<hipEvent_t> events;
+  // Filtered profiling (ndx_model_set_profile_filter): only nodes of one
+  // kernel family are bracketed, from a pool of events that grows across
+  // runs; nothing waits until the entries are read.
+  std::string prof_filter;
+  std::vector<std::string> node_family;  // per node, made when profiling starts
+  std::vector<hipEvent_t> fevents;
+  std::vector<int> prof_pending;  // node of each bracketed launch, in record order
   // Two lanes: per node, the latest node of each lane it must wait for (-1
   // none), the event a node records for others (-1 none), and the events.
   bool two_lanes = false;
@@ -1223,7 +1230,11 @@ static void plan_lanes(ndx_model* m, const std::vector<int>& last) {
     for (int t = 0; t < 2; t++)
       if (m->waits[i][t] >= 0 && m->signal[m->waits[i][t]] < 0) m->signal[m->waits[i][t]] = ne++;
   m->lane_events.resize(ne + 2);
-  for (auto& e : m->lane_events) hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+  // Both lanes are on this device: a device-scope release makes a lane's
+  // writes visible to the other (all XCDs), without the system-scope cache
+  // writeback a default event does.
+  for (auto& e : m->lane_events)
+    hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventReleaseToDevice), "hipEventCreate");
 }
 
 extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* outputs, int32_t count,
@@ -1925,10 +1936,13 @@ void run_nodes(ndx_model* m, Runner& r) {
     hip_check(hipEventRecord(m->lane_events[ne - 2], s), "hipEventRecord");
     hip_check(hipStreamWaitEvent(st[1], m->lane_events[ne - 2], 0), "hipStreamWaitEvent");
   }
+  const bool filtered = m->profiling && !m->prof_filter.empty();
+  const bool full = m->profiling && !filtered;
   size_t need = m->nodes.size() * 2;
-  while (m->profiling && m->events.size() < need) {
+  while (full && m->events.size() < need) {
     hipEvent_t e;
-    hip_check(hipEventCreate(&e), "hipEventCreate");
+    // Timing only: no cache writeback when recorded (it would slow what follows).
+    hip_check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
     m->events.push_back(e);
   }
   for (size_t i = 0; i < m->nodes.size(); i++) {
@@ -1938,9 +1952,24 @@ void run_nodes(ndx_model* m, Runner& r) {
       for (int t = 0; t < 2; t++)
         if (m->waits[i][t] >= 0)
           hip_check(hipStreamWaitEvent(ns, m->lane_events[m->signal[m->waits[i][t]]], 0), "hipStreamWaitEvent");
-    if (m->profiling) hip_check(hipEventRecord(m->events[2 * i], ns), "hipEventRecord");
+    const bool bracket = filtered && !(n.op == OP_LINEAR && n.i5 == 2) && m->node_family[i] == m->prof_filter;
+    const size_t fe = 2 * m->prof_pending.size();
+    if (bracket) {
+      while (m->fevents.size() < fe + 2) {
+        hipEvent_t e;
+        // Timing only: no cache writeback when recorded (it would slow what follows).
+    hip_check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
+        m->fevents.push_back(e);
+      }
+      hip_check(hipEventRecord(m->fevents[fe], ns), "hipEventRecord");
+    }
+    if (full) hip_check(hipEventRecord(m->events[2 * i], ns), "hipEventRecord");
     r.launch(n, ns);
-    if (m->profiling) hip_check(hipEventRecord(m->events[2 * i + 1], ns), "hipEventRecord");
+    if (full) hip_check(hipEventRecord(m->events[2 * i + 1], ns), "hipEventRecord");
+    if (bracket) {
+      hip_check(hipEventRecord(m->fevents[fe + 1], ns), "hipEventRecord");
+      m->prof_pending.push_back((int)i);
+    }
     if (m->two_lanes && m->signal[i] >= 0)
       hip_check(hipEventRecord(m->lane_events[m->signal[i]], ns), "hipEventRecord");
   }
@@ -1948,39 +1977,66 @@ void run_nodes(ndx_model* m, Runner& r) {
     hip_check(hipEventRecord(m->lane_events[ne - 1], st[1]), "hipEventRecord");
     hip_check(hipStreamWaitEvent(s, m->lane_events[ne - 1], 0), "hipStreamWaitEvent");
   }
-  if (!m->profiling) {
+  if (!full) {
     hip_check(hipGetLastError(), "kernel launch");
     return;
   }
   hip_check(hipGetLastError(), "kernel launch");
   hip_check(hipStreamSynchronize(s), "profiled run");
   for (size_t i = 0; i < m->nodes.size(); i++) {
+    const GNode& n = m->nodes[i];
+    if (n.op == OP_LINEAR && n.i5 == 2) continue;  // timed with the node before it
     float ms = 0;
     hip_check(hipEventElapsedTime(&ms, m->events[2 * i], m->events[2 * i + 1]), "hipEventElapsedTime");
-    const GNode& n = m->nodes[i];
-    std::string fam = n.family;
-    if (n.op == OP_LINEAR) {
-      if (n.i5 == 2) continue;  // timed with the node before it
-      auto probe = [&](const GNode& k) {
-        GemmArgs p{};
-        const GValue& x = m->values[k.in[0]];
-        const GValue& w = m->values[k.in[1]];
-        p.a_dtype = x.dtype;
-        p.w_dtype = w.quant ? NDX_I8 : w.dtype;
-        p.M = (int)(x.v.size[2]);
-        p.N = (int)w.v.size[2];
-        p.K = (int)x.v.size[3];
-        p.batch = (int)(x.v.size[0] * x.v.size[1]);
-        return p;
-      };
-      fam = n.i5 == 1 ? gemm_pair_family(probe(n), probe(m->nodes[i + 1])) : gemm_family(probe(n));
-    }
-    ProfEntry& e = m->prof[fam];
+    ProfEntry& e = m->prof[m->node_family[i]];
     e.launches++;
     e.ms += ms;
     e.flops += n.flops;
     e.bytes += n.bytes;
   }
+}
+
+// The kernel family of each node, as profiles name them (a pair of linears
+// launched together under the first node).
+void compute_families(ndx_model* m) {
+  m->node_family.assign(m->nodes.size(), std::string());
+  auto probe = [&](const GNode& k) {
+    GemmArgs p{};
+    const GValue& x = m->values[k.in[0]];
+    const GValue& w = m->values[k.in[1]];
+    p.a_dtype = x.dtype;
+    p.w_dtype = w.quant ? NDX_I8 : w.dtype;
+    p.M = (int)(x.v.size[2]);
+    p.N = (int)w.v.size[2];
+    p.K = (int)x.v.size[3];
+    p.batch = (int)(x.v.size[0] * x.v.size[1]);
+    return p;
+  };
+  for (size_t i = 0; i < m->nodes.size(); i++) {
+    const GNode& n = m->nodes[i];
+    std::string fam = n.family;
+    if (n.op == OP_LINEAR && n.i5 != 2)
+      fam = n.i5 == 1 ? gemm_pair_family(probe(n), probe(m->nodes[i + 1])) : gemm_family(probe(n));
+    m->node_family[i] = fam;
+  }
+}
+
+// Waits for the filtered brackets recorded so far and adds them up.
+void harvest_filtered(ndx_model* m) {
+  if (m->prof_pending.empty()) return;
+  hip_check(hipStreamSynchronize(m->dev->stream), "profiled runs");
+  for (size_t k = 0; k < m->prof_pending.size(); k++) {
+    const int i = m->prof_pending[k];
+    float ms = 0;
+    hip_check(hipEventElapsedTime(&ms, m->fevents[2 * k], m->fevents[2 * k + 1]), "hipEventElapsedTime");
+    const GNode& n = m->nodes[i];
+    ProfEntry& e = m->prof[m->node_family[i]];
+    e.launches++;
+    e.ms += ms;
+    e.flops += n.flops + (n.op == OP_LINEAR && n.i5 == 1 ? m->nodes[i + 1].flops : 0.0);
+    e.bytes += n.bytes + (n.op == OP_LINEAR && n.i5 == 1 ? m->nodes[i + 1].bytes : 0.0);
+  }
+  m->prof_pending.clear();
 }
 
 }  // namespace
@@ -2071,8 +2127,20 @@ NDX_API ndx_status ndx_model_run_into_async(ndx_model* m, ndx_tensor* const* inp
 NDX_API ndx_status ndx_model_set_profiling(ndx_model* m, int32_t enabled) {
   NDX_TRY
   NEED(m);
+  harvest_filtered(m);
   m->profiling = enabled != 0;
-  if (m->profiling) m->prof.clear();
+  if (m->profiling) {
+    m->prof.clear();
+    if (m->node_family.size() != m->nodes.size()) compute_families(m);
+  }
+  NDX_CATCH
+}
+
+NDX_API ndx_status ndx_model_set_profile_filter(ndx_model* m, const char* family) {
+  NDX_TRY
+  NEED(m);
+  harvest_filtered(m);
+  m->prof_filter = family ? family : "";
   NDX_CATCH
 }
 
@@ -2080,6 +2148,7 @@ NDX_API ndx_status ndx_model_profile_entry(ndx_model* m, int32_t index, char* na
                                            int64_t* launches, double* ms, double* flops, double* bytes) {
   NDX_TRY
   NEED(m);
+  harvest_filtered(m);
   if (index < 0 || index >= (int)m->prof.size()) fail(NDX_INVALID_ARG, "no such profile entry");
   auto it = m->prof.begin();
   std::advance(it, index);
@@ -2100,6 +2169,7 @@ NDX_API ndx_status ndx_model_release(ndx_model* m) {
   }
   if (m->two_lanes && m->dev->aux) (void)hipStreamSynchronize(m->dev->aux);
   for (auto e : m->events) (void)hipEventDestroy(e);
+  for (auto e : m->fevents) (void)hipEventDestroy(e);
   for (auto e : m->lane_events) (void)hipEventDestroy(e);
   delete m;
   NDX_CATCH

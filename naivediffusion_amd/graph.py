@@ -380,7 +380,10 @@ class CompiledModel:
             o.Dispose()
         return host
 
-    def SetProfiling(self, enabled: bool) -> None:
+    def SetProfiling(self, enabled: bool, family: Optional[str] = None) -> None:
+        """Per-kernel timing. family: bracket only that kernel family's
+        launches, with no wait per run (for a timed region)."""
+        call("ndx_model_set_profile_filter", self.handle, family.encode() if family else None)
         call("ndx_model_set_profiling", self.handle, int(enabled))
 
     def Profile(self) -> dict:
