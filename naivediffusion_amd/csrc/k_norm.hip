@@ -204,6 +204,87 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
   }
 }
 
+// Compile-time-typed loads and stores for the fast row-norm kernel.
+template <int DT>
+__device__ __forceinline__ float4 load4_t(const void* p, int64_t i) {
+  if constexpr (DT == NDX_F32) {
+    return *(const float4*)((const float*)p + i);
+  } else {
+    const uint2 u = *(const uint2*)((const uint16_t*)p + i);
+    if constexpr (DT == NDX_BF16) {
+      return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                         __uint_as_float(u.y & 0xffff0000u));
+    } else {
+      const _Float16* h = (const _Float16*)&u;
+      return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ void store4_t(void* p, int64_t i, float4 v) {
+  if constexpr (DT == NDX_F32) {
+    *(float4*)((float*)p + i) = v;
+  } else if constexpr (DT == NDX_BF16) {
+    __bf16 h[4] = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+    *(uint2*)((__bf16*)p + i) = *(const uint2*)h;
+  } else {
+    _Float16 h[4] = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    *(uint2*)((_Float16*)p + i) = *(const uint2*)h;
+  }
+}
+
+// row_norm_vec_kernel for fp32 rows and fp32 affine terms (the residual
+// stream's norms: Modulate, LayerNorm, RmsNorm) with the output type fixed at
+// compile time: the row, the weight and the bias are all requested before
+// the statistics are reduced, and nothing in the loops branches on a type,
+// so a wave has its whole row and affine terms in flight at once.
+template <int NC, int YT>
+__global__ __launch_bounds__(256) void row_norm_f32_kernel(RowNormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t batch = row / a.rows_per_batch;
+  const int64_t xoff = batch * a.batch_x + (row % a.rows_per_batch) * a.ldx;
+  constexpr int D = NC * 256;
+  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  float4 v[NC], w[NC], bb[NC];
+#pragma unroll
+  for (int j = 0; j < NC; j++) v[j] = load4_t<NDX_F32>(a.x, xoff + (j * 64 + lane) * 4);
+  const bool hw = a.weight != nullptr, hb = a.bias != nullptr;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const int c = (j * 64 + lane) * 4;
+    w[j] = hw ? load4_t<NDX_F32>(a.weight, woff + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    bb[j] = hb ? load4_t<NDX_F32>(a.bias, boff + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float mean = 0.f;
+  if (a.mode != 2) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    mean = wave_sum(s) * (1.0f / D);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
+    ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) * (1.0f / D) + a.eps);
+  const int64_t yoff = row * a.ldy;
+  // Modulate scales by (1 + scale); the others by the weight when there is one.
+  const float w1 = a.mode == 1 ? 1.0f : 0.0f;
+#pragma unroll
+  for (int j = 0; j < NC; j++) {
+    const int c = (j * 64 + lane) * 4;
+    float4 n = make_float4((v[j].x - mean) * rstd, (v[j].y - mean) * rstd, (v[j].z - mean) * rstd,
+                           (v[j].w - mean) * rstd);
+    if (hw) n = make_float4(n.x * (w1 + w[j].x), n.y * (w1 + w[j].y), n.z * (w1 + w[j].z), n.w * (w1 + w[j].w));
+    if (hb) n = make_float4(n.x + bb[j].x, n.y + bb[j].y, n.z + bb[j].z, n.w + bb[j].w);
+    store4_t<YT>(a.y, yoff + c, n);
+  }
+}
+
 static bool vec_ok(const void* p, int dt, int64_t ld, int64_t batch) {
   if (!p) return true;
   const int es = dtype_size(dt);
@@ -219,6 +300,21 @@ void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
   const bool vec = a.D % 256 == 0 && a.D <= 4096 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) &&
                    vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, 0, a.batch_w) &&
                    vec_ok(a.bias, a.b_dtype, 0, a.batch_b);
+  const bool f32_terms = a.x_dtype == NDX_F32 && (!a.weight || a.w_dtype == NDX_F32) &&
+                         (!a.bias || a.b_dtype == NDX_F32);
+  if (vec && f32_terms && (a.D == 2048 || a.D == 3072 || a.D == 4096)) {
+#define NDX_RN(NC)                                                                                        \
+  do {                                                                                                    \
+    if (a.y_dtype == NDX_BF16) hipLaunchKernelGGL((row_norm_f32_kernel<NC, NDX_BF16>), grid, block, 0, s, a); \
+    else if (a.y_dtype == NDX_F16) hipLaunchKernelGGL((row_norm_f32_kernel<NC, NDX_F16>), grid, block, 0, s, a); \
+    else hipLaunchKernelGGL((row_norm_f32_kernel<NC, NDX_F32>), grid, block, 0, s, a);                       \
+  } while (0)
+    if (a.D == 2048) NDX_RN(8);
+    else if (a.D == 3072) NDX_RN(12);
+    else NDX_RN(16);
+#undef NDX_RN
+    return;
+  }
   if (vec) {
     switch (a.D / 256) {
       case 1: hipLaunchKernelGGL(row_norm_vec_kernel<1>, grid, block, 0, s, a); return;
