@@ -9,10 +9,10 @@
 // the output and the row sum are per-lane registers and one exchange with
 // lane l ^ 32. The output is accumulated transposed, O^T += V^T P^T, with P^T
 // fed straight from the score registers: the key order inside each 16-key
-// MFMA step is permuted identically on both operands, so V^T is read from
-// LDS in that order and no score ever leaves registers. K and V^T tiles of 64
-// keys are double buffered in LDS (V transposed on its way in), swizzled by
-// 16- and 8-byte granules.
+// MFMA step is permuted identically on both operands, so no score ever
+// leaves registers. K and V tiles of 64 keys arrive by DMA into row-major,
+// chunk-swizzled LDS, double buffered; the V^T operand comes out of LDS
+// through gfx950's transposing ds_read_b64_tr_b16, in the score order.
 //
 // flash_attn_f32_kernel (fp32, d = 64 or 128): the same scheme on fp32
 // MFMA, described at the kernel.
@@ -70,26 +70,35 @@ __device__ __forceinline__ bool attn_tile(int pid, int grid, int qblocks, int H,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// LDS layouts of the key tile (64 rows of D elements) and the transposed
-// value tile (D rows of 64 keys), swizzled for gfx950's LDS: 64 four-byte
-// banks, a 16-byte read served sixteen lanes at a time and an 8-byte read
-// thirty-two at a time. The fragment reads put those lanes on consecutive
-// rows at one logical granule; the XOR keys below put them on distinct
-// banks. Keys: 16-byte chunk c of row `key`.
+// LDS layouts of the key and value tiles: 64 rows of D elements each, row
+// major as in memory (both arrive by DMA), swizzled by 16-byte chunk for
+// gfx950's LDS (64 four-byte banks; a 16-byte read is served sixteen lanes
+// at a time, an 8-byte read thirty-two at a time). Chunk c of row `key`
+// sits at chunk c ^ x(key).
+// Keys are read 16 bytes per lane, sixteen consecutive rows at one chunk:
+// x = key % 16 at D = 128; at D = 64 rows are 128 bytes, so rows r and r + 1
+// share the bank span and x = (key / 2) % 8.
 template <int D>
-__device__ __forceinline__ int k_off(int key, int c) {
-  // D = 128: a row is 256 bytes, chunk c ^ (key % 16) is distinct over 16
-  // rows. D = 64: rows are 128 bytes, so rows r and r + 1 share the bank
-  // span; the key is (key / 2) % 8 together with the row's half.
-  const int x = D == 128 ? (key & 15) : ((key >> 1) & 7);
-  return key * D + ((c ^ x) << 3);
+__device__ __forceinline__ int k_swz(int key) {
+  return D == 128 ? (key & 15) : ((key >> 1) & 7);
 }
-// Values: 8-byte group g (4 keys) of row d. Rows are 128 bytes; 32 lanes
-// read rows d .. d + 31, so the group is XORed with ((d / 2) ^ (d / 8)) % 16,
-// a bijection over the 16 rows of each parity; the writes (rows 8 i + 2 e
-// of sixteen lanes, see store_v) are distinct under it too.
-__device__ __forceinline__ int vt_off(int d, int g) {
-  return d * 64 + ((g ^ (((d >> 1) ^ (d >> 3)) & 15)) << 2);
+// Values are read by the transposing ds_read_b64_tr_b16: thirty-two lanes
+// cover four consecutive rows, 64 bytes (four chunks) of each. x = 4 (key % 4)
+// at D = 128 puts each row's four chunks on their own 16 banks; at D = 64
+// rows r and r + 1 already sit on different halves and x = 4 ((key / 2) % 2)
+// separates r and r + 2.
+template <int D>
+__device__ __forceinline__ int v_swz(int key) {
+  return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2);
+}
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane L supplies the address
+// of four 16-bit elements (row L / 4 of a 4 x 16 block, columns 4 (L % 4) ..
+// 4 (L % 4) + 3); lane j receives column j of the block, rows 0..3.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(p)));
 }
 
 // One tile: 128 queries (4 waves x 32) of one (batch, head) over key blocks
@@ -97,6 +106,11 @@ __device__ __forceinline__ int vt_off(int d, int g) {
 // writes the normalised output; otherwise it leaves its unnormalised O^T
 // registers, running max and partial row sum in `part` (field-major, one
 // float per thread per field) for attn_combine_kernel.
+//
+// K and V blocks are double buffered in four distinct LDS arrays (K0/V0 for
+// even blocks, K1/V1 for odd): the DMA of block kb + 1 starts when block kb
+// does, and since its destination is a different restrict pointer from
+// every array read during block kb, no LDS read has to wait for it.
 //
 // Softmax: the running max is kept over raw scores, so a probability is one
 // fused multiply-add (score * scale * log2 e - max) and one v_exp_f32
@@ -107,15 +121,14 @@ __device__ __forceinline__ int vt_off(int d, int g) {
 // past the end get -inf.
 template <typename T, int D, int MASK>
 __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int head, int b, int kb0, int kb1,
-                                               float* part, T (*__restrict__ Ks)[64 * D],
-                                               T (*__restrict__ Vt)[D * 64]) {
+                                               float* part, T* __restrict__ K0, T* __restrict__ K1,
+                                               T* __restrict__ V0, T* __restrict__ V1) {
   typedef typename AMfma<T>::V V;
   constexpr int BQ = 128, BKEY = 64;
-  constexpr int KCH = D / 8;                      // 16-byte chunks per key row
-  constexpr int V_TASKS = (BKEY / 4) * (D / 8);   // (4-key group, 8-d chunk) tasks
+  constexpr int KCH = D / 8;                      // 16-byte chunks per row
   constexpr int DT = D / 32;                      // output tiles along d
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, lh = lane >> 5;
   const int64_t col0 = int64_t(head) * D;
   const int qi = qb * BQ + wave * 32 + lq;
@@ -129,102 +142,57 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int s = 0; s < D / 16; s++) qf[s] = *(const V*)(qrow + s * 16 + lh * 8);
   }
 
-  // K goes global -> LDS by DMA (buffer_load ... lds): a wave-wide load
+  // K and V go global -> LDS by DMA (buffer_load ... lds): a wave-wide load
   // fills one kilobyte, KROWS rows; lane l lands at byte 16 l (row l / (D/8)
   // of the group, physical chunk l % (D/8)) and fetches the logical chunk
-  // that k_off places there. V goes through registers (it is transposed on
-  // its way into LDS).
-  constexpr int KROWS = 512 / D;            // key rows per kilobyte load
-  constexpr int K_LOADS = BKEY / KROWS / 4; // loads per wave per block
-  const int kr = lane / (D / 8), kpc = lane % (D / 8);
-  int kcol[K_LOADS];
+  // that the swizzle places there.
+  constexpr int KROWS = 512 / D;            // rows per kilobyte load
+  constexpr int LOADS = BKEY / KROWS / 4;   // loads per wave per block and tensor
+  const int kr = lane / KCH, kpc = lane % KCH;
+  int kcol[LOADS], vcol[LOADS];
 #pragma unroll
-  for (int i = 0; i < K_LOADS; i++) {
-    const int key = (wave * K_LOADS + i) * KROWS + kr;
-    const int x = D == 128 ? (key & 15) : ((key >> 1) & 7);
-    kcol[i] = (int)col0 + ((kpc ^ x) << 3);
+  for (int i = 0; i < LOADS; i++) {
+    const int key = (wave * LOADS + i) * KROWS + kr;
+    kcol[i] = (int)col0 + ((kpc ^ k_swz<D>(key)) << 3);
+    vcol[i] = (int)col0 + ((kpc ^ v_swz<D>(key)) << 3);
   }
-  uint4 rv[4];
-  const int vkg = tid / (D / 8), vdc = tid % (D / 8);
   // (Offsets fit in 32 bits when a row stride is below 2^24 elements.)
   const bool small_ld = a.k.ld[0] < (1 << 24) && a.k.ld[1] < (1 << 24) && a.v.ld[0] < (1 << 24) &&
                         a.v.ld[1] < (1 << 24);
-  // The base of key block kb in segment sg of s: blocks inside one segment
-  // (and the whole block below S, for V) take one uniform base. Ternaries,
-  // not s.ptr[sg]: a runtime index into the kernel arguments makes the
-  // compiler fetch them from memory on every block.
-  auto seg_base = [&](const AttnSeg& sgm, int key0, bool second) -> const T* {
-    return second ? (const T*)sgm.ptr[1] + b * sgm.batch[1] + (key0 - sgm.rows0) * sgm.ld[1]
-                  : (const T*)sgm.ptr[0] + b * sgm.batch[0] + key0 * sgm.ld[0];
-  };
-  auto issue_k = [&](int kb, int buf) {
+  // Block kb of one tensor into `buf`. The base of a block inside one
+  // segment is uniform. Ternaries, not s.ptr[sg]: a runtime index into the
+  // kernel arguments makes the compiler fetch them from memory every block.
+  auto issue = [&](const AttnSeg& sg, T* buf, int kb, const int (&col)[LOADS], bool value) {
     const int key0 = kb * BKEY;
-    const bool second = key0 >= a.k.rows0;
-    if (small_ld && (second || key0 + BKEY <= a.k.rows0)) {
-      // Rows past the keys (or past the segment) read as zeros.
-      const int64_t end = second ? a.S : std::min<int64_t>(a.k.rows0, a.S);
+    const bool second = key0 >= sg.rows0;
+    if (small_ld && (second || key0 + BKEY <= sg.rows0)) {
+      // Rows past the keys (or past the segment) read as zeros: a zero
+      // value row keeps 0 * stale from turning into NaN, and a zero key row
+      // is masked like every key past the end.
+      const int64_t end = second ? a.S : std::min<int64_t>(sg.rows0, a.S);
       const int rows = (int)std::min<int64_t>(BKEY, end - key0);
-      const int64_t ld = second ? a.k.ld[1] : a.k.ld[0];
-      const __amdgpu_buffer_rsrc_t rk = make_rsrc(seg_base(a.k, key0, second), uint32_t(rows * ld * 2));
+      const int64_t ld = second ? sg.ld[1] : sg.ld[0];
+      const T* base = second ? (const T*)sg.ptr[1] + b * sg.batch[1] + (key0 - sg.rows0) * sg.ld[1]
+                             : (const T*)sg.ptr[0] + b * sg.batch[0] + key0 * sg.ld[0];
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(base, uint32_t(rows * ld * 2));
 #pragma unroll
-      for (int i = 0; i < K_LOADS; i++) {
-        const int key = (wave * K_LOADS + i) * KROWS + kr;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&Ks[buf][(wave * K_LOADS + i) * KROWS * D], 16,
-                                                 uint32_t((key * ld + kcol[i]) * 2), 0, 0, 0);
+      for (int i = 0; i < LOADS; i++) {
+        const int key = (wave * LOADS + i) * KROWS + kr;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)&buf[(wave * LOADS + i) * KROWS * D], 16,
+                                                 uint32_t((key * ld + col[i]) * 2), 0, 0, 0);
       }
       return;
     }
     // A block across the two segments (or huge strides): chunk by chunk
-    // through registers.
+    // through registers; value rows past the keys are zeroed.
 #pragma unroll 1
     for (int i = 0; i < BKEY * KCH / 256; i++) {
       const int id = tid + i * 256;
       const int key = id / KCH, c = id % KCH;
-      const int gk = min(key0 + key, a.S - 1);  // tail keys are masked below
-      *(uint4*)&Ks[buf][k_off<D>(key, c)] = *(const uint4*)(seg_row<T>(a.k, b, gk) + col0 + c * 8);
-    }
-  };
-  // V rows through registers, branch free (a branch here would make the
-  // compiler copy the loaded registers at the join, waiting for the loads):
-  // the row is clamped into the keys and its segment picked by selects;
-  // rows past the keys are zeroed when stored.
-  const int64_t v_ld0 = a.v.ld[0], v_ld1 = a.v.ld[1];
-  const T* v_base0 = (const T*)a.v.ptr[0] + b * a.v.batch[0] + col0 + vdc * 8;
-  const T* v_base1 = (const T*)a.v.ptr[1] + b * a.v.batch[1] - a.v.rows0 * a.v.ld[1] + col0 + vdc * 8;
-  auto load_v = [&](int kb) {
-    if (tid >= V_TASKS) return;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int gk = min(kb * BKEY + vkg * 4 + e, a.S - 1);
-      const T* p = gk < a.v.rows0 ? v_base0 + gk * v_ld0 : v_base1 + gk * v_ld1;
-      rv[e] = *(const uint4*)p;
-    }
-  };
-  auto store_v = [&](int buf, int kb) {
-    if (tid < V_TASKS) {
-      // Tail rows must be zero: a zero probability times a stale value
-      // could still be NaN.
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (kb * BKEY + vkg * 4 + e >= a.S) rv[e] = make_uint4(0, 0, 0, 0);
-      const uint32_t w0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
-      const uint32_t w1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
-      const uint32_t w2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
-      const uint32_t w3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
-      // Threads of odd key groups write their odd row first, so each write
-      // instruction covers both row parities (all 64 banks).
-      const int odd = vkg & 1;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        // Two d rows per 32-bit word: (d, d+1) of keys 4g..4g+3.
-        const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x05040100),
-                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100));
-        const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[e], w0[e], 0x07060302),
-                                    __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302));
-        const int d = vdc * 8 + 2 * e;
-        *(uint2*)&Vt[buf][vt_off(d + odd, vkg)] = odd ? hi : lo;
-        *(uint2*)&Vt[buf][vt_off(d + 1 - odd, vkg)] = odd ? lo : hi;
-      }
+      const int gk = min(key0 + key, a.S - 1);
+      uint4 x = *(const uint4*)(seg_row<T>(sg, b, gk) + col0 + c * 8);
+      if (value && key0 + key >= a.S) x = make_uint4(0, 0, 0, 0);
+      *(uint4*)&buf[key * D + ((c ^ (value ? v_swz<D>(key) : k_swz<D>(key))) << 3)] = x;
     }
   };
 
@@ -242,39 +210,38 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
 
   // Byte offsets of this lane's fragment reads within one buffer. Keys:
   // step s reads chunk 2 s + lh of row lq (the second 32-key tile is 32 rows
-  // on); the swizzle key of row kt * 32 + lq does not depend on kt. Values:
-  // d = dt * 32 + lq and group g = 4 u + 2 p + lh; the swizzle key of row d
-  // is that of row lq with bit 2 flipped by dt, so the read offset depends on
-  // (u ^ dt, p) and dt only adds 32 rows.
+  // on); the swizzle of row kt * 32 + lq does not depend on kt. Values: for
+  // the 16-key step u, output tile dt and half h, lane L of 16-lane group g
+  // addresses row 16 u + 8 h + kl, kl = 4 (g / 2) + L / 4, at d = 32 dt +
+  // 16 (g % 2) + 4 (L % 4): the transposed read then hands lane l the values
+  // of d = 32 dt + l % 32 at keys 16 u + 8 h + 4 (l / 32) + 0..3, which are
+  // the keys of the score registers that P^T takes its operand from. The
+  // swizzle depends on kl only, so u and h are immediates.
   constexpr int NSD = D / 16;
-  int kq[NSD], vq[8];
+  int kq[NSD], vq[DT];
   {
-    const int kx = D == 128 ? (lq & 15) : ((lq >> 1) & 7);
+    const int kx = k_swz<D>(lq);
 #pragma unroll
     for (int s2 = 0; s2 < NSD; s2++) kq[s2] = (lq * D + (((2 * s2 + lh) ^ kx) << 3)) * 2;
-    const int vx = ((lq >> 1) ^ (lq >> 3)) & 15;
+    const int g = lane >> 4, L = lane & 15;
+    const int kl = 4 * (g >> 1) + (L >> 2);
+    const int vx = v_swz<D>(kl) >> 2;
 #pragma unroll
-    for (int w = 0; w < 8; w++) vq[w] = (lq * 64 + ((((w >> 1) << 2) | ((w & 1) << 1) | lh) ^ vx) * 4) * 2;
+    for (int dt = 0; dt < DT; dt++)
+      vq[dt] = kl * D * 2 + ((((dt ^ vx) << 2) | ((g & 1) << 1) | ((L >> 1) & 1)) << 4) + ((L & 1) << 3);
   }
-  issue_k(kb0, 0);
-  load_v(kb0);
-  store_v(0, kb0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kb = kb0; kb < kb1; kb++) {
-    const int cur = (kb - kb0) & 1;
-    // Block kb + 1 goes into the other buffers, whose last reads (block
-    // kb - 1) every wave finished before the previous barrier: V into
-    // registers now, K by DMA once this block's key fragments are read (an
-    // LDS read after a DMA into the same array waits for the DMA; Ks and Vt
-    // are distinct restrict pointers, so the value reads below do not).
-    if (kb + 1 < kb1) load_v(kb + 1);
 
+  // Block kb from Kc/Vc, with block kb + 1 on its way into Kn/Vn.
+  auto block = [&](int kb, const T* Kc, const T* Vc, T* Kn, T* Vn) {
+    if (kb + 1 < kb1) {
+      issue(a.k, Kn, kb + 1, kcol, false);
+      issue(a.v, Vn, kb + 1, vcol, true);
+    }
     // S^T for 64 keys: two 32-key tiles (raw scores), the key fragment of
     // the next step read under the current step's MFMA.
     f32x16 sacc[2];
     {
-      const char* kbuf = (const char*)Ks[cur];
+      const char* kbuf = (const char*)Kc;
       V kf[2];
       kf[0] = *(const V*)(kbuf + kq[0]);
 #pragma unroll
@@ -285,7 +252,6 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
         sacc[kt] = AMfma<T>::mma(kf[i & 1], qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     }
-    if (kb + 1 < kb1) issue_k(kb + 1, cur ^ 1);
     if (MASK != NDX_MASK_NONE || (kb + 1) * BKEY > a.S) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
@@ -334,13 +300,21 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], sl, -m_new));
-        sacc[kt][r] = p;
-        l_part += p;
-      }
+      for (int r = 0; r < 16; r++) sacc[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], sl, -m_new));
+    // The block's row sum as a pairwise tree (short dependency chains).
+    {
+      float t[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) t[r] = sacc[0][r] + sacc[1][r];
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int r = 0; r < w; r++) t[r] += t[r + w];
+      l_part += t[0];
+    }
 
     // O^T += V^T P^T over four 16-key steps.
+    const char* vbuf = (const char*)Vc;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       V pb;
@@ -348,18 +322,25 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
       for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) {
-        const char* vrow = (const char*)Vt[cur] + dt * 4096;
-        const uint2 x1 = *(const uint2*)(vrow + vq[((u ^ dt) << 1) | 0]);
-        const uint2 x2 = *(const uint2*)(vrow + vq[((u ^ dt) << 1) | 1]);
-        const V vf = __builtin_bit_cast(V, make_uint4(x1.x, x1.y, x2.x, x2.y));
+        const uint2 x0 = lds_read_tr16(vbuf + vq[dt] + (u * 16) * D * 2);
+        const uint2 x1 = lds_read_tr16(vbuf + vq[dt] + (u * 16 + 8) * D * 2);
+        const V vf = __builtin_bit_cast(V, make_uint4(x0.x, x0.y, x1.x, x1.y));
         o[dt] = AMfma<T>::mma(vf, pb, o[dt]);
       }
     }
-    if (kb + 1 < kb1) store_v(cur ^ 1, kb + 1);
     // This wave's DMA of block kb + 1 has landed; after the barrier, every
-    // wave's has.
+    // wave's has, and every wave is done reading block kb.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+
+  issue(a.k, K0, kb0, kcol, false);
+  issue(a.v, V0, kb0, vcol, true);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kb = kb0; kb < kb1; kb += 2) {
+    block(kb, K0, V0, K1, V1);
+    if (kb + 1 < kb1) block(kb + 1, K1, V1, K0, V0);
   }
 
   if (part) {
@@ -414,12 +395,14 @@ __device__ __forceinline__ void decode_tile(int t, int qblocks, int H, int& qb, 
 template <typename T, int D, int MASK>
 __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, AttnSched sc) {
   constexpr int DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ks[2][64 * D];
-  __shared__ __attribute__((aligned(16))) T Vt[2][D * 64];
+  __shared__ __attribute__((aligned(1024))) T K0[64 * D];
+  __shared__ __attribute__((aligned(1024))) T K1[64 * D];
+  __shared__ __attribute__((aligned(1024))) T V0[64 * D];
+  __shared__ __attribute__((aligned(1024))) T V1[64 * D];
   int qb, head, b;
   if (!sc.split) {
     if (!attn_tile(blockIdx.x, sc.grid, sc.qblocks, a.H, a.B, qb, head, b)) return;
-    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, Ks, Vt);
+    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, K0, K1, V0, V1);
     return;
   }
   const int w = blockIdx.x;
@@ -427,14 +410,14 @@ __global__ __launch_bounds__(256, 2) void flash_attn_kernel(AttnArgs a, AttnSche
     // Consecutive tiles (the query blocks of one head) to one XCD.
     const int t = (w % 8) * (sc.head_tiles / 8) + w / 8;
     decode_tile(t, sc.qblocks, a.H, qb, head, b);
-    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, Ks, Vt);
+    attn_tile_body<T, D, MASK>(a, qb, head, b, 0, sc.KB, nullptr, K0, K1, V0, V1);
     return;
   }
   const int p = w - sc.head_tiles;
   const int ti = p / sc.ps, k = p % sc.ps;
   decode_tile(sc.head_tiles + ti, sc.qblocks, a.H, qb, head, b);
   attn_tile_body<T, D, MASK>(a, qb, head, b, k * sc.KB / sc.ps, (k + 1) * sc.KB / sc.ps,
-                             sc.part + int64_t(p) * ((DT * 16 + 2) * 256), Ks, Vt);
+                             sc.part + int64_t(p) * ((DT * 16 + 2) * 256), K0, K1, V0, V1);
 }
 
 // Merges the ps partials of tail tile blockIdx.x, columns d in [32 y,
