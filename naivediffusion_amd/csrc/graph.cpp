@@ -78,6 +78,15 @@ struct GNode {
 
 int64_t numel4(const View4& v) { return v.size[0] * v.size[1] * v.size[2] * v.size[3]; }
 
+// The tile of a linear on the second stream. The latency model picks small
+// tiles for a product of few rows (many short workgroups finish soonest on
+// an idle GPU); beside the first stream's large products, though, what
+// counts is how many CU-cycles the product takes from them, and 128x128
+// tiles do the same work in about two thirds of the CU time of 64x64 ones
+// (the MMDiT text stream: 2% less step time on MI355X; 256x256 tiles hold
+// CUs so long that the other stream's rounds stall).
+int second_stream_tile(const GNode& n, int64_t rows) { return n.lane == 1 && rows >= 128 ? 2 : 0; }
+
 View4 packed4(const int64_t* size) {
   View4 v;
   for (int i = 0; i < 4; i++) v.size[i] = size[i];
@@ -1586,6 +1595,7 @@ struct Runner {
       a.w_dtype = w.dtype;
     }
     a.batch_w = 0;
+    a.tile_hint = second_stream_tile(n, a.M);
     a.c = ptr(n.out);
     a.ldc = a.N;
     a.batch_c = int64_t(a.M) * a.N;
@@ -2010,13 +2020,19 @@ void compute_families(ndx_model* m) {
     p.N = (int)w.v.size[2];
     p.K = (int)x.v.size[3];
     p.batch = (int)(x.v.size[0] * x.v.size[1]);
+    p.tile_hint = second_stream_tile(k, p.M);
     return p;
   };
+  // NDX_PROFILE_LANES=1 names the second stream's kernels apart ("@lane1"),
+  // to see what each stream spends; read when profiling is switched on.
+  const char* by_lane = getenv("NDX_PROFILE_LANES");
+  const bool lanes = by_lane && by_lane[0] == '1';
   for (size_t i = 0; i < m->nodes.size(); i++) {
     const GNode& n = m->nodes[i];
     std::string fam = n.family;
     if (n.op == OP_LINEAR && n.i5 != 2)
       fam = n.i5 == 1 ? gemm_pair_family(probe(n), probe(m->nodes[i + 1])) : gemm_family(probe(n));
+    if (lanes && n.lane == 1) fam += "@lane1";
     m->node_family[i] = fam;
   }
 }

@@ -1231,7 +1231,7 @@ static GemmKind choose(const GemmArgs& a) {
     static const GemmKind lds[4] = {K_LDS_256W8, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
     static const GemmKind w8[4] = {K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64};
     static const GemmKind reg[4] = {K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64};
-    const int t = pick_tile(a.M, a.N, a.K, a.batch);
+    const int t = a.tile_hint >= 1 && a.tile_hint <= 4 ? a.tile_hint - 1 : pick_tile(a.M, a.N, a.K, a.batch);
     if (a.w_dtype != NDX_I8) return lds[t];
     // The direct-to-LDS int8 kernel takes one scale per 32 columns.
     return a.qblock % 32 == 0 ? w8[t] : reg[t];

@@ -78,6 +78,9 @@ struct GemmArgs {
   // batch_w elements per image) at taps (ky, kx) of a kw-wide filter whose
   // K index is (ky * kw + kx) * Cin + ci.
   int conv_cin, conv_h, conv_w, conv_wo, conv_kw, conv_stride, conv_pad;
+  // The 16-bit tile to use regardless of the latency model (0: the model;
+  // 1..4: 256x256, 128x128, 64x128, 64x64).
+  int tile_hint;
 };
 
 // DmlOps.Gemm in full generality (any strides, transposes, alpha, beta): a
