@@ -659,8 +659,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
 // DmlOps.Dequantize's output is (Graph/ModelBuilder.cs:28-35). Scales are
 // per (row, qblock columns): BlockQuantizer's 32 (fp16), or the whole row
 // (per output channel, fp32).
+//
+// The dequantisation is software pipelined: while the MFMAs of tile kt run,
+// each thread turns tile kt + 1's int8 into bf16, one 8-column chunk per
+// 16-deep MFMA step, so the VALU work hides under the matrix cores instead of
+// running between barriers with the MFMAs idle. Tile kt + 1's A and tile
+// kt + 2's int8 are DMA'd when iteration kt starts and waited for when it
+// ends. The six tiles (A, int8 and bf16, two of each) are distinct restrict
+// pointers and the loop is unrolled by two, so no LDS read waits for a DMA
+// into another tile; at 256 x 256 they fill the 160 KB of LDS.
 template <int BM, int BN, int WM, int WN, typename T, bool SF16>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel(GemmArgs a, int grid) {
+__device__ __forceinline__ void gemm_w8_body(const GemmArgs& a, int grid, T* __restrict__ A0, T* __restrict__ A1,
+                                             int8_t* __restrict__ Q0, int8_t* __restrict__ Q1,
+                                             T* __restrict__ B0, T* __restrict__ B1, float* stage_all) {
   typedef typename MfmaOp<T>::V V;
   constexpr int WAVES_N = BN / WN;
   constexpr int NW = (BM / WM) * (BN / WN), NT = NW * 64;
@@ -668,21 +679,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
   constexpr int A_LOADS = BM / 8 / NW;    // kilobyte loads of A per wave per tile (8 rows x 128 B)
   constexpr int W_LOADS = BN / 16 / NW;   // kilobyte loads of W per wave per tile (16 rows x 64 B)
   static_assert(A_LOADS * 8 * NW == BM && W_LOADS * 16 * NW == BN, "tile rows do not split over the waves");
-  constexpr int A_BYTES = 2 * BM * BK * (int)sizeof(T);
-  constexpr int W8_BYTES = 2 * BN * BK;
-  constexpr int B_BYTES = BN * BK * (int)sizeof(T);
-  constexpr int TILE_BYTES = A_BYTES + W8_BYTES + B_BYTES;
-  constexpr int STAGE_BYTES = NW * 32 * (WN + 4) * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
-  T (*As)[BM * BK] = reinterpret_cast<T (*)[BM * BK]>(smem);
-  int8_t (*W8s)[BN * BK] = reinterpret_cast<int8_t (*)[BN * BK]>(smem + A_BYTES);
-  T* Bs = reinterpret_cast<T*>(smem + A_BYTES + W8_BYTES);
 
   int tm, tn;
   if (!tile_of(blockIdx.x, grid, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn)) return;
   const int64_t bidx = blockIdx.y;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   constexpr int ES = (int)sizeof(T);
 
@@ -708,31 +710,29 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
     w_row[i] = n0 + r < a.N ? (uint32_t)(int64_t(n0 + r) * a.ldw) : kOutOfRange;
   }
 
-  auto issue_tile = [&](int kt, int buf) {
+  auto issue_a = [&](int kt, T* buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; i++) {
       const int k = kt * BK + kchunk_q[(wave * A_LOADS + i) & 1] * 8;
       const uint32_t off = (k < a.K && a_row[i] != kOutOfRange) ? a_row[i] + uint32_t(k * ES) : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&As[buf][(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&buf[(wave * A_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
     }
+  };
+  auto issue_q = [&](int kt, int8_t* buf) __attribute__((always_inline)) {
     const int kw = kt * BK + wchunk * 16;
     const bool kwin = kw < a.K;
 #pragma unroll
     for (int i = 0; i < W_LOADS; i++) {
       const uint32_t off = (kwin && w_row[i] != kOutOfRange) ? w_row[i] + uint32_t(kw) : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&W8s[buf][(wave * W_LOADS + i) * 16 * BK], 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&buf[(wave * W_LOADS + i) * 16 * BK], 16, off, 0, 0, 0);
     }
   };
 
-  // Dequant tasks: (row r, columns [32 h, 32 h + 32)) for task 2 r + h,
-  // one scale each (qblock is a multiple of 32). The scales of tile kt + 1
-  // are loaded during tile kt, before its DMA is issued: vector memory
-  // completes in order, so a scale loaded after the DMA would make the
-  // dequant wait for the whole next tile.
-  // The scale's raw bits (fp16 or fp32 by SF16) travel to the next
-  // iteration unconverted, so nothing waits on the load until then.
+  // Dequant tasks: (row r, columns [32 h, 32 h + 32)) for task 2 r + h, one
+  // scale each (qblock is a multiple of 32). A scale's raw bits (fp16 or
+  // fp32 by SF16) are loaded an iteration ahead and converted only when used.
   constexpr int TPT = (2 * BN + NT - 1) / NT;  // tasks per thread
-  auto load_scales = [&](int kt, uint32_t (&raw)[TPT]) {
+  auto load_scales = [&](int kt, uint32_t (&raw)[TPT]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < TPT; t++) {
       const int task = tid + t * NT, dr = task >> 1, k0 = kt * BK + (task & 1) * 32;
@@ -742,29 +742,40 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
       else raw[t] = in ? ((const uint32_t*)a.scales)[i] : 0u;
     }
   };
-  auto dequant = [&](int buf, const float (&scs)[TPT]) {
+  auto to_float = [&](const uint32_t (&raw)[TPT], float (&sc)[TPT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < TPT; t++)
+      sc[t] = SF16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)raw[t]) : __uint_as_float(raw[t]);
+  };
+  // The 32 int8 of every task of this thread. (Read before the iteration's
+  // DMA is issued: an LDS access after it would wait for the DMA.)
+  auto read_q = [&](const int8_t* q, uint4 (&qv)[TPT][2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < TPT; t++) {
       const int task = tid + t * NT;
-      // (A branch here only where the tasks do not fill the threads: a
-      // divergent branch before the LDS reads makes the compiler wait for
-      // the next tile's DMA.)
       if (NT * TPT != 2 * BN && task >= 2 * BN) break;
       const int dr = task >> 1, dh = task & 1;
-      const float sc = scs[t];
-      const uint4 q0 = *(const uint4*)&W8s[buf][dr * BK + dh * 32];
-      const uint4 q1 = *(const uint4*)&W8s[buf][dr * BK + dh * 32 + 16];
-      const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      qv[t][0] = *(const uint4*)&q[dr * BK + dh * 32];
+      qv[t][1] = *(const uint4*)&q[dr * BK + dh * 32 + 16];
+    }
+  };
+  // Chunk c (columns 8 c .. 8 c + 7 of the task's 32) of every task of this
+  // thread, from the registers read_q filled, into the swizzled bf16 tile.
+  auto dequant_chunk = [&](T* b, const float (&sc)[TPT], const uint4 (&qv)[TPT][2], int c) __attribute__((always_inline)) {
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        T h[8];
+    for (int t = 0; t < TPT; t++) {
+      const int task = tid + t * NT;
+      if (NT * TPT != 2 * BN && task >= 2 * BN) break;
+      const int dr = task >> 1, dh = task & 1;
+      const uint4 x = qv[t][c >> 1];
+      const uint32_t w[2] = {(c & 1) ? x.z : x.x, (c & 1) ? x.w : x.y};
+      T h[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const int v = (int)(int8_t)((w[2 * c + e / 4] >> (8 * (e & 3))) & 0xff);
-          h[e] = (T)((float)v * sc);
-        }
-        *(uint4*)&Bs[swz(dr, dh * 4 + c)] = *(const uint4*)h;
+      for (int e = 0; e < 8; e++) {
+        const int v = (int)(int8_t)((w[e / 4] >> (8 * (e & 3))) & 0xff);
+        h[e] = (T)((float)v * sc[t]);
       }
+      *(uint4*)&b[swz(dr, dh * 4 + c)] = *(const uint4*)h;
     }
   };
 
@@ -778,71 +789,120 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
 
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int KT = (a.K + BK - 1) / BK;
-  uint32_t sc_next[TPT];
-  load_scales(0, sc_next);
-  issue_tile(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; kt++) {
-    const int cur = kt & 1;
-    // This tile's scales arrived with the previous tile's loads: convert
-    // them before this iteration issues any load.
-    float sc_cur[TPT];
+  uint32_t sc_raw[TPT];
+  {
+    // A of tile 0, the int8 of tiles 0 and 1 and their scales; tile 0
+    // dequantised.
+    uint32_t raw0[TPT];
+    load_scales(0, raw0);
+    issue_a(0, A0);
+    issue_q(0, Q0);
+    issue_q(1, Q1);
+    load_scales(1, sc_raw);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    float sc0[TPT];
+    to_float(raw0, sc0);
+    uint4 qv[TPT][2];
+    read_q(Q0, qv);
 #pragma unroll
-    for (int t = 0; t < TPT; t++)
-      sc_cur[t] = SF16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)sc_next[t]) : __uint_as_float(sc_next[t]);
-    // Dequantise before the next tile's DMA is in flight (an LDS read after
-    // it would wait for it), then issue that DMA to overlap the MFMAs. The
-    // barrier waits only for the LDS writes (lgkmcnt 0), not the DMA.
-    dequant(cur, sc_cur);
-    load_scales(kt + 1, sc_next);
-    issue_tile(kt + 1, cur ^ 1);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
+    for (int c = 0; c < 4; c++) dequant_chunk(B0, sc0, qv, c);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // Iteration kt: the MFMAs of tile kt (Ac, Bc) with tile kt + 1's int8 (Qd)
+  // dequantised into Bn under them; tile kt + 1's A goes to An and tile
+  // kt + 2's int8 to Qn.
+  constexpr int NF = TM + TN, NM = TM * TN, NS = BK / 16;
+  auto iter = [&](int kt, const T* Ac, const T* Bc, T* An, const int8_t* Qd, T* Bn, int8_t* Qn) __attribute__((always_inline)) {
+    float sc[TPT];
+    to_float(sc_raw, sc);
+    uint4 qv[TPT][2];
+    read_q(Qd, qv);
+    issue_a(kt + 1, An);
+    issue_q(kt + 2, Qn);
+    load_scales(kt + 2, sc_raw);
     V af[2][TM], bf[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, lhalf)];
+    for (int i = 0; i < TM; i++) af[0][i] = *(const V*)&Ac[swz(wm * WM + i * 32 + lrow, lhalf)];
 #pragma unroll
-    for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bs[swz(wn * WN + j * 32 + lrow, lhalf)];
+    for (int j = 0; j < TN; j++) bf[0][j] = *(const V*)&Bc[swz(wn * WN + j * 32 + lrow, lhalf)];
 #pragma unroll
-    for (int s = 0; s < BK / 16; s++) {
+    for (int s = 0; s < NS; s++) {
       const int p = s & 1;
-      if (s + 1 < BK / 16) {
+      if (s + 1 < NS) {
         const int c = 2 * (s + 1) + lhalf;
 #pragma unroll
-        for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&As[cur][swz(wm * WM + i * 32 + lrow, c)];
+        for (int i = 0; i < TM; i++) af[p ^ 1][i] = *(const V*)&Ac[swz(wm * WM + i * 32 + lrow, c)];
 #pragma unroll
-        for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bs[swz(wn * WN + j * 32 + lrow, c)];
+        for (int j = 0; j < TN; j++) bf[p ^ 1][j] = *(const V*)&Bc[swz(wn * WN + j * 32 + lrow, c)];
       }
+      dequant_chunk(Bn, sc, qv, s);
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[p][i], bf[p][j], acc[i][j]);
     }
-    // Each step's MFMAs with the next step's fragment reads threaded
-    // between them, as in the 16-bit kernel.
-    constexpr int NF = TM + TN, NM = TM * TN;
-    __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
-#pragma unroll
-    for (int s = 0; s < BK / 16 - 1; s++) {
-      if (NM >= NF) {
-#pragma unroll
-        for (int f = 0; f < NF; f++) {
-          __builtin_amdgcn_sched_group_barrier(0x0008, NM / NF, 0);
-          __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);
-        }
-      } else {
-        __builtin_amdgcn_sched_group_barrier(0x0100, NF, 0);
-        __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
-      }
-    }
-    __builtin_amdgcn_sched_group_barrier(0x0008, NM, 0);
+    // Tile kt + 1 (A and the bf16 just written) and tile kt + 2's int8 are
+    // complete for every wave after this.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+  for (int kt = 0; kt < KT; kt += 2) {
+    iter(kt, A0, B0, A1, Q1, B1, Q0);
+    if (kt + 1 < KT) iter(kt + 1, A1, B1, A0, Q0, B0, Q1);
   }
 
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
+  // Each wave's epilogue stage: in an array of its own (stage_all), or, when
+  // the tiles can hold every wave's, inside them (the loop is done with
+  // them): as many per tile as fit, A tiles first, then bf16, then int8.
+  constexpr int SW = 32 * (WN + 4);
+  constexpr int CA = BM * BK * (int)sizeof(T) / (SW * 4), CB = BN * BK * (int)sizeof(T) / (SW * 4);
+  constexpr int CQ = BN * BK / (SW * 4);
+  float* stage;
+  if (stage_all) {
+    stage = stage_all + wave * SW;
+  } else {
+    int w = wave;
+    float* const bases[6] = {reinterpret_cast<float*>(A0), reinterpret_cast<float*>(A1), reinterpret_cast<float*>(B0),
+                             reinterpret_cast<float*>(B1), reinterpret_cast<float*>(Q0), reinterpret_cast<float*>(Q1)};
+    const int caps[6] = {CA, CA, CB, CB, CQ, CQ};
+    stage = bases[0];
+#pragma unroll
+    for (int t = 0; t < 6; t++) {
+      if (w >= 0 && w < caps[t]) stage = bases[t] + w * SW;
+      w -= caps[t];
+    }
+  }
   staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+}
+
+// Every tile is an LDS array of its own: the compiler orders an LDS access
+// after a DMA only against the arrays the DMA may write, and tells distinct
+// arrays apart (slices of one array it cannot), so no read or write of one
+// tile waits for the DMA into another. At 256 x 256 the six tiles fill the
+// 160 KB of LDS; the epilogue stages in the tiles wherever they can hold
+// every wave's stage.
+template <int BM, int BN, int WM, int WN, typename T, bool SF16>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel(GemmArgs a, int grid) {
+  constexpr int NW = (BM / WM) * (BN / WN);
+  constexpr int TILES = 2 * (BM * BK * (int)sizeof(T) + BN * BK + BN * BK * (int)sizeof(T));
+  constexpr int SWB = 32 * (WN + 4) * 4;
+  constexpr int CAP = 2 * (BM * BK * (int)sizeof(T) / SWB + BN * BK * (int)sizeof(T) / SWB + BN * BK / SWB);
+  static_assert(TILES <= 160 * 1024 && (CAP >= NW || TILES + NW * SWB <= 160 * 1024), "tiles exceed the LDS");
+  __shared__ __attribute__((aligned(1024))) T a0[BM * BK];
+  __shared__ __attribute__((aligned(1024))) T a1[BM * BK];
+  __shared__ __attribute__((aligned(1024))) int8_t q0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) int8_t q1[BN * BK];
+  __shared__ __attribute__((aligned(1024))) T b0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) T b1[BN * BK];
+  if constexpr (CAP >= NW) {
+    gemm_w8_body<BM, BN, WM, WN, T, SF16>(a, grid, a0, a1, q0, q1, b0, b1, nullptr);
+  } else {
+    __shared__ __attribute__((aligned(1024))) float st[NW * SWB / 4];
+    gemm_w8_body<BM, BN, WM, WN, T, SF16>(a, grid, a0, a1, q0, q1, b0, b1, st);
+  }
 }
 
 // ---- fp32 -------------------------------------------------------------------
@@ -1471,9 +1531,9 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
     case K_LDS_256W8: launch_mfma_lds<256, 256, 64, 128>(a, s); break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
-    case K_W8_256W8: launch_w8_lds<256, 256, 64, 128>(a, s); break;
+    case K_W8_256W8: launch_w8_lds<256, 256, 128, 64>(a, s); break;
     case K_W8_128: launch_w8_lds<128, 128, 64, 64>(a, s); break;
-    case K_W8_64x128: launch_w8_lds<64, 128, 32, 64>(a, s); break;
+    case K_W8_64x128: launch_w8_lds<64, 128, 64, 32>(a, s); break;
     case K_W8_64x64: launch_w8_lds<64, 64, 32, 32>(a, s); break;
     case K_F32: {
       int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
