@@ -115,7 +115,8 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
 // Softmax: the running max is kept over raw scores, so a probability is one
 // fused multiply-add (score * scale * log2 e - max) and one v_exp_f32
 // (2^x; results below 2^-126 flush to zero, far below a bf16 probability's
-// resolution). Masks and the key tail change the raw scores in a uniform
+// resolution); the max in use may trail the true one by up to 2^8 (see the
+// rescale below). Masks and the key tail change the raw scores in a uniform
 // branch (only the masked kernels and the last key block take it): a ruled-
 // out key gets -10000 / scale added, i.e. -10000 after scaling, and keys
 // past the end get -inf.
@@ -285,18 +286,24 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
         for (int r = 0; r < 16; r++) mx = fminf(mx, sacc[kt][r]);
     }
     const float mloc = mx * sl;
-    const float m_new = fmaxf(m_run, fmaxf(mloc, __shfl_xor(mloc, 32, 64)));
-    // Rescale the running output only when some lane's max moved: after
-    // the first blocks the maxima settle and the multiply is skipped.
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float m_blk = fmaxf(m_run, fmaxf(mloc, __shfl_xor(mloc, 32, 64)));
+    // The max subtracted in the exponent may lag the true running max by up
+    // to 8 (log2 units): probabilities then reach at most 2^8, exact in fp32
+    // and bf16, and the output and row sum carry the same factor, so the
+    // result is unchanged. The rescale of the output (64 multiplies) runs
+    // only when some lane's max grows by more than that, which after the
+    // first blocks is rare, instead of whenever any of the wave's 32 queries
+    // meets a new maximum.
+    if (__builtin_amdgcn_ballot_w64(m_blk > m_run + 8.0f)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_blk);
       l_part *= alpha;
 #pragma unroll
       for (int j = 0; j < DT; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+      m_run = m_blk;
     }
-    m_run = m_new;
+    const float m_new = m_run;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
