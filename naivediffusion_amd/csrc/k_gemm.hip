@@ -1529,7 +1529,7 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
-    case K_LDS_256W8: launch_mfma_lds<256, 256, 64, 128>(a, s); break;
+    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s); break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
     case K_W8_256W8: launch_w8_lds<256, 256, 128, 64>(a, s); break;
     case K_W8_128: launch_w8_lds<128, 128, 64, 64>(a, s); break;
