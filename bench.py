@@ -75,9 +75,10 @@ def read_traffic(kernel, workload):
     return None, None
 
 
-def cpu_baseline(device, cfg, seed, ni, nt):
+def cpu_baseline(device, cfg, seed, ni, nt, grid=(64, 84), batch=1):
     """The oracle (the C restatement of the reference's CpuMath layer path,
-    fp32, OpenMP) on one block of the same step, scaled to cfg.blocks."""
+    fp32, OpenMP) on one block of the same step (one batch element, a grid
+    of image tokens), scaled to cfg.blocks x batch."""
     import oracle
     from naivediffusion_amd import mmdit, rng
     from naivediffusion_amd.tensors import HostDataType as DT
@@ -99,7 +100,7 @@ def cpu_baseline(device, cfg, seed, ni, nt):
     xi = device.Normal(DT.Float32, [ni, D], rng.tensor_seed(seed, "cpu.x_img")).Download().ToFloats()
     xt = device.Normal(DT.Float32, [nt, D], rng.tensor_seed(seed, "cpu.x_txt")).Download().ToFloats()
     temb = device.Normal(DT.Float32, [D], rng.tensor_seed(seed, "cpu.temb")).Download().ToFloats()
-    cos, sin = mmdit.rope_tables(64, 84, nt)
+    cos, sin = mmdit.rope_tables(grid[0], grid[1], nt)
     oracle.lib()
     threads = len(os.sched_getaffinity(0))
     log(f"cpu baseline: one block on the oracle, {threads} threads")
@@ -114,13 +115,14 @@ def cpu_baseline(device, cfg, seed, ni, nt):
                 break
     except OSError:
         pass
+    per = f" x{batch} batch elements" if batch > 1 else ""
     return {
-        "value": dt * cfg.blocks,
+        "value": dt * cfg.blocks * batch,
         "unit": "s/step",
         "cores": threads,
         "kind": "port",
         "sample": (f"one MMDiT block ({ni} image + {nt} text tokens, hidden {D}, fp32) on the oracle's C restatement "
-                   f"of the reference CpuMath layer path in {dt:.2f} s, x{cfg.blocks} blocks (extrapolated); "
+                   f"of the reference CpuMath layer path in {dt:.2f} s, x{cfg.blocks} blocks{per} (extrapolated); "
                    f"host CPU: {cpu_model}"),
     }
 
@@ -191,34 +193,39 @@ def setup_mmdit(args, dev, seed, DT):
 
     cfg = mmdit.MmditConfig(blocks=args.blocks or 60)
     compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
-    lat_h, lat_w, nt = 128, 168, 256
-    ni = (lat_h // cfg.patch) * (lat_w // cfg.patch)
+    img_h, img_w = (int(v) for v in args.image.lower().split("x"))
+    if img_h % 16 or img_w % 16:
+        sys.exit("--image sides must be multiples of 16 (8x VAE, 2x2 patch)")
+    B, lat_h, lat_w, nt = args.batch, img_h // 8, img_w // 8, 256
+    gh, gw = lat_h // cfg.patch, lat_w // cfg.patch
+    ni = gh * gw
     t0 = time.perf_counter()
     weights = mmdit.device_weights(dev, cfg, seed)
     log(f"synthetic weights on the device in {time.perf_counter() - t0:.1f} s")
-    model = mmdit.build_step_model(dev, cfg, weights, 1, nt, lat_h, lat_w, compute, args.int8)
+    model = mmdit.build_step_model(dev, cfg, weights, B, nt, lat_h, lat_w, compute, args.int8)
     n = ni + nt
-    cos, sin = mmdit.rope_tables(lat_h // cfg.patch, lat_w // cfg.patch, nt)
+    cos, sin = mmdit.rope_tables(gh, gw, nt)
+    temb = np.tile(mmdit.time_embedding(0.5, cfg.time_dim), (B, 1)).reshape(B, 1, 1, cfg.time_dim)
     inputs = [
-        dev.Normal(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w], rng.tensor_seed(seed, "latent")),
-        dev.Normal(DT.Float32, [1, 1, nt, cfg.text_dim], rng.tensor_seed(seed, "text")),
-        dev.Upload(HostTensor.FromFloats(mmdit.time_embedding(0.5, cfg.time_dim).reshape(1, 1, 1, cfg.time_dim))),
+        dev.Normal(DT.Float32, [B, cfg.latent_channels, lat_h, lat_w], rng.tensor_seed(seed, "latent")),
+        dev.Normal(DT.Float32, [B, 1, nt, cfg.text_dim], rng.tensor_seed(seed, "text")),
+        dev.Upload(HostTensor.FromFloats(np.ascontiguousarray(temb, np.float32))),
         dev.Upload(HostTensor.FromFloats(cos.reshape(1, n, 1, 64))),
         dev.Upload(HostTensor.FromFloats(sin.reshape(1, n, 1, 64))),
     ]
-    out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat_h, lat_w])]
+    out = [dev.Empty(DT.Float32, [B, cfg.latent_channels, lat_h, lat_w])]
     wdesc = {None: f"{args.compute} weights", "block32": "int8 weights, fp16 scales per 32 columns",
              "channel": "int8 weights, fp32 scales per output channel"}[args.int8]
     return dict(
         model=model, inputs=inputs, out=out,
         metric="Qwen-Image DiT s/step @1024x1344 (bf16/int8 wts), 1 MI355X; % MFMA peak",
-        config={"workload": (f"Qwen-Image-shaped MMDiT denoiser step, {cfg.blocks} dual-stream blocks, 1024x1344 "
-                             f"(latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), hidden 3072, "
-                             f"24x128 heads, MLP 12288, batch 1, {args.compute} compute, {wdesc}"),
-                "blocks": cfg.blocks, "image_tokens": ni, "text_tokens": nt,
+        config={"workload": (f"Qwen-Image-shaped MMDiT denoiser step, {cfg.blocks} dual-stream blocks, "
+                             f"{img_h}x{img_w} (latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), "
+                             f"hidden 3072, 24x128 heads, MLP 12288, batch {B}, {args.compute} compute, {wdesc}"),
+                "blocks": cfg.blocks, "image_tokens": ni, "text_tokens": nt, "batch": B,
                 "weights": f"int8-{args.int8}" if args.int8 else args.compute},
         data="synthetic (seeded N(0,1) latent and text, N(0,0.02) bf16 weights made on the GPU)",
-        cpu=lambda: cpu_baseline(dev, cfg, seed, ni, nt),
+        cpu=lambda: cpu_baseline(dev, cfg, seed, ni, nt, (gh, gw), B),
     )
 
 
@@ -317,6 +324,9 @@ def main():
                     help="int8 weights: block32 (the reference's BlockQuantizer format, the default) or channel "
                          "(one fp32 scale per output channel)")
     ap.add_argument("--blocks", type=int, default=None, help="block count (default: the model's)")
+    ap.add_argument("--image", default="1024x1344", help="mmdit: image size HxW (1328x1328 with --batch 2 and "
+                    "--int8 channel is the CFG int8 configuration)")
+    ap.add_argument("--batch", type=int, default=1, help="mmdit: batch (2: cond + uncond CFG)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")
     args = ap.parse_args()
@@ -332,6 +342,8 @@ def main():
         return
     if args.compute is None:
         args.compute = "f16" if args.workload == "sdxl" else "bf16"
+    if args.workload != "mmdit" and (args.batch != 1 or args.image != "1024x1344"):
+        sys.exit("--image and --batch apply to the mmdit workload only")
 
     import naivediffusion_amd as nd
     from naivediffusion_amd.tensors import HostDataType as DT
