@@ -58,9 +58,109 @@ static int grid_for(int64_t total, int threads) {
   return (int)blocks;
 }
 
+// Eight consecutive elements of type DT as fp32, and back.
+template <int DT>
+__device__ __forceinline__ void ld8(const void* p, int64_t i, float (&o)[8]) {
+  if constexpr (DT == NDX_F32) {
+    const float4 x = *(const float4*)((const float*)p + i), y = *(const float4*)((const float*)p + i + 4);
+    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+  } else {
+    const uint4 u = *(const uint4*)((const uint16_t*)p + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if constexpr (DT == NDX_BF16) {
+        o[2 * e] = __uint_as_float(w[e] << 16);
+        o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+      } else {
+        o[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffff));
+        o[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
+      }
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ void st8(void* p, int64_t i, const float (&v)[8]) {
+  if constexpr (DT == NDX_F32) {
+    *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)((float*)p + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else if constexpr (DT == NDX_BF16) {
+    __bf16 h[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (__bf16)v[e];
+    *(uint4*)((__bf16*)p + i) = *(const uint4*)h;
+  } else {
+    _Float16 h[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (_Float16)v[e];
+    *(uint4*)((_Float16*)p + i) = *(const uint4*)h;
+  }
+}
+
+// The elementwise op over eight consecutive innermost elements per thread,
+// every tensor of type DT: the output packed, the first input's innermost
+// axis contiguous, the second's contiguous or broadcast (stride 0), every
+// row start a multiple of eight elements. Index arithmetic once per eight
+// elements in 32 bits, 16-byte loads and stores, no type switch per load:
+// the generic kernel's per-element 64-bit divisions and typed loads held it
+// near 1.2 TB/s on SDXL's GEGLU and broadcast adds.
+template <int DT>
+__global__ __launch_bounds__(256) void elementwise_vec_kernel(ElemArgs a, int chunks) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int s3 = (int)a.vo.size[3] >> 3, s2 = (int)a.vo.size[2], s1 = (int)a.vo.size[1];
+  int r = c;
+  const int i3 = (r % s3) * 8;
+  r /= s3;
+  const int i2 = r % s2;
+  r /= s2;
+  const int i1 = r % s1;
+  const int i0 = r / s1;
+  float x[8], y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  ld8<DT>(a.in0, offset_of(a.v0, i0, i1, i2, i3), x);
+  if (a.in1) {
+    const int64_t o1 = offset_of(a.v1, i0, i1, i2, i3);
+    if (a.v1.stride[3] == 0) {
+      const float b = load_f(a.in1, DT, o1);
+#pragma unroll
+      for (int e = 0; e < 8; e++) y[e] = b;
+    } else {
+      ld8<DT>(a.in1, o1, y);
+    }
+  }
+  float z[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) z[e] = apply_elem(a.op, x[e], y[e], a.scale, a.bias);
+  st8<DT>(a.out, int64_t(c) * 8, z);
+}
+
+static bool vec_view(const View4& v, bool allow_splat) {
+  if (allow_splat && v.stride[3] == 0) return true;  // one scalar load per eight outputs
+  if (v.stride[3] != 1) return false;
+  for (int d = 0; d < 3; d++)
+    if (v.stride[d] % 8) return false;
+  return true;
+}
+
 void launch_elementwise(const ElemArgs& a, hipStream_t s) {
   int64_t total = a.vo.size[0] * a.vo.size[1] * a.vo.size[2] * a.vo.size[3];
   if (total == 0) return;
+  const View4& o = a.vo;
+  const bool packed_out = o.stride[3] == 1 && o.stride[2] == o.size[3] && o.stride[1] == o.size[2] * o.size[3] &&
+                          o.stride[0] == o.size[1] * o.size[2] * o.size[3];
+  const int dt = a.dto;
+  const int es = dtype_size(dt);
+  const bool typed = (dt == NDX_F16 || dt == NDX_BF16 || dt == NDX_F32) && a.dt0 == dt && (!a.in1 || a.dt1 == dt);
+  if (typed && packed_out && o.size[3] % 8 == 0 && total / 8 < (int64_t(1) << 31) && vec_view(a.v0, false) &&
+      (!a.in1 || vec_view(a.v1, true)) && (uintptr_t)a.out % 16 == 0 && (uintptr_t)a.in0 % 16 == 0 &&
+      (!a.in1 || a.v1.stride[3] == 0 || (uintptr_t)a.in1 % 16 == 0) && es > 0) {
+    const int chunks = (int)(total / 8);
+    const dim3 g((unsigned)((chunks + 255) / 256));
+    if (dt == NDX_F16) hipLaunchKernelGGL((elementwise_vec_kernel<NDX_F16>), g, dim3(256), 0, s, a, chunks);
+    else if (dt == NDX_BF16) hipLaunchKernelGGL((elementwise_vec_kernel<NDX_BF16>), g, dim3(256), 0, s, a, chunks);
+    else hipLaunchKernelGGL((elementwise_vec_kernel<NDX_F32>), g, dim3(256), 0, s, a, chunks);
+    return;
+  }
   hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
 }
 

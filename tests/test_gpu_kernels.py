@@ -614,3 +614,55 @@ def test_paired_linears_run_as_one_launch(device, M1, M2, K, N):
     assert rel_err(o1, e1) <= BF16_TOL
     assert rel_err(o2 - r2, e2 - r2) <= BF16_TOL
     assert rel_err(o3, e3) <= BF16_TOL
+
+
+def _round(x, dtype):
+    x = np.asarray(x, np.float32)
+    if dtype == DT.BFloat16:
+        return bf(x)
+    if dtype == DT.Float16:
+        return x.astype(np.float16).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16, DT.Float32])
+def test_elementwise_vector_and_generic_paths(device, dtype):
+    """Elementwise ops over rows whose length is a multiple of 8 (the
+    vectorised kernel: a row slice times GELU of the other half, as SDXL's
+    GEGLU; a per-channel broadcast add, as its time embedding; unary and
+    binary ops on packed rows) and over ragged rows (the generic kernel),
+    against numpy on the same rounded inputs."""
+    print(f"[gpu] elementwise paths {dtype.name}", flush=True)
+    B, C, H, W, n, inner = 2, 6, 5, 40, 7, 48
+    p_h = _round(normal("ep", (B, 1, n, 2 * inner)), dtype)
+    x_h = _round(normal("ex", (B, C, H, W)), dtype)
+    t_h = _round(normal("et", (B, C, 1, 1)), dtype)
+    r_h = _round(normal("er", (B, 1, 3, 21)), dtype)
+    g = nd.Graph(device)
+    proj = g.Input(dtype, [B, 1, n, 2 * inner])
+    x = g.Input(dtype, [B, C, H, W])
+    t = g.Input(dtype, [B, C, 1, 1])
+    r = g.Input(dtype, [B, 1, 3, 21])
+    a = Ops.Slice(proj, [0, 0, 0, 0], [B, 1, n, inner])
+    b = Ops.Slice(proj, [0, 0, 0, inner], [B, 1, n, inner])
+    outs = [a * Ops.ActivationGelu(b), x + Layers.Broadcast(t, [B, C, H, W]), Ops.ActivationSwish(x),
+            Ops.Divide(x, Ops.ActivationSigmoid(x)), Ops.Subtract(x, x * 0.5), r * r + r]
+    m = nd.CompiledModel(g, outs, device)
+
+    def host(v):
+        ht = HostTensor.FromFloats(v)
+        return ht if dtype == DT.Float32 else ht.ConvertTo(dtype)
+
+    got = [o.ToFloats().reshape(e.shape) for o, e in zip(
+        m.Dispatch([host(p_h), host(x_h), host(t_h), host(r_h)]),
+        [p_h[..., :inner], x_h, x_h, x_h, x_h, r_h])]
+    a_n, b_n = p_h[..., :inner], p_h[..., inner:]
+    gelu = lambda v: 0.5 * v * (1.0 + np.vectorize(math.erf)(v / math.sqrt(2.0)))
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+    ref = [a_n * _round(gelu(b_n), dtype), x_h + t_h, x_h * sig(x_h), x_h / _round(sig(x_h), dtype),
+           x_h - _round(x_h * 0.5, dtype), _round(r_h * r_h, dtype) + r_h]
+    tol = 1e-5 if dtype == DT.Float32 else 1.5e-2
+    for k, (o, e) in enumerate(zip(got, ref)):
+        err = rel_err(o, e)
+        print(f"[gpu]   output {k}: rel err {err:.2e}", flush=True)
+        assert err <= tol, (k, err)
