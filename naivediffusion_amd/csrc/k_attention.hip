@@ -583,16 +583,19 @@ __global__ __launch_bounds__(256) void flash_attn_f32_kernel(AttnArgs a, int gri
         mloc = fmaxf(mloc, x);
       }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
-      const float alpha = exp2f(m_run - m_new);
+    // The lazy rescale of the 16-bit kernel: the max in use may trail the
+    // running max by up to 8 (log2 units).
+    const float m_blk = fmaxf(m_run, mloc);
+    if (__builtin_amdgcn_ballot_w64(m_blk > m_run + 8.0f)) {
+      const float alpha = exp2f(m_run - m_blk);
       l_part *= alpha;
 #pragma unroll
       for (int j = 0; j < DT; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[j][r] *= alpha;
+      m_run = m_blk;
     }
-    m_run = m_new;
+    const float m_new = m_run;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
