@@ -29,11 +29,25 @@ namespace ndx {
 
 template <typename T>
 struct AMfma;
+// mma: the 32x32x16 MFMA. sum8: acc plus the eight elements of a fragment,
+// as four two-element dot products with (1, 1) (v_dot2_f32_bf16 / _f16):
+// half the VALU instructions of eight adds.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 template <>
 struct AMfma<__bf16> {
   typedef bf16x8 V;
   static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float sum8(V v, float acc) {
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const bf16x2_t pr = {v[2 * j], v[2 * j + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
   }
 };
 template <>
@@ -41,6 +55,15 @@ struct AMfma<_Float16> {
   typedef f16x8 V;
   static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float sum8(V v, float acc) {
+    const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const f16x2_t pr = {v[2 * j], v[2 * j + 1]};
+      acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
   }
 };
 
@@ -202,7 +225,10 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
   for (int j = 0; j < DT; j++)
 #pragma unroll
     for (int r = 0; r < 16; r++) o[j][r] = 0.f;
-  float m_run = -INFINITY, l_part = 0.f;
+  float m_run = -INFINITY;
+  // Row sums of the rounded probabilities (the values the output is weighted
+  // with), one partial per 16-key step so the dot-product chains stay short.
+  float lp[4] = {0.f, 0.f, 0.f, 0.f};
   const float sl = a.scale * kLog2e;
   const bool pos = sl > 0.f;
   const float mask_raw = -10000.0f / a.scale;
@@ -296,7 +322,8 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     // meets a new maximum.
     if (__builtin_amdgcn_ballot_w64(m_blk > m_run + 8.0f)) {
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_blk);
-      l_part *= alpha;
+#pragma unroll
+      for (int u = 0; u < 4; u++) lp[u] *= alpha;
 #pragma unroll
       for (int j = 0; j < DT; j++)
 #pragma unroll
@@ -308,17 +335,6 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) sacc[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], sl, -m_new));
-    // The block's row sum as a pairwise tree (short dependency chains).
-    {
-      float t[16];
-#pragma unroll
-      for (int r = 0; r < 16; r++) t[r] = sacc[0][r] + sacc[1][r];
-#pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-        for (int r = 0; r < w; r++) t[r] += t[r + w];
-      l_part += t[0];
-    }
 
     // O^T += V^T P^T over four 16-key steps.
     const char* vbuf = (const char*)Vc;
@@ -327,6 +343,7 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
       V pb;
 #pragma unroll
       for (int j = 0; j < 8; j++) pb[j] = (T)sacc[u >> 1][(u & 1) * 8 + j];
+      lp[u] = AMfma<T>::sum8(pb, lp[u]);
 #pragma unroll
       for (int dt = 0; dt < DT; dt++) {
         const uint2 x0 = lds_read_tr16(vbuf + vq[dt] + (u * 16) * D * 2);
@@ -350,6 +367,7 @@ __device__ __forceinline__ void attn_tile_body(const AttnArgs& a, int qb, int he
     if (kb + 1 < kb1) block(kb + 1, K1, V1, K0, V0);
   }
 
+  const float l_part = (lp[0] + lp[1]) + (lp[2] + lp[3]);
   if (part) {
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
