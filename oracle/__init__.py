@@ -3,9 +3,9 @@ of NaiveDiffusion's CPU layer math (Tensors/CpuMath.cs), its int8 block
 quantiser (Tensors/BlockQuantizer.cs), the Transformer helpers
 (Graph/Transformer.cs) and the DirectML operator semantics the graphs use.
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
-the checker, and by bench.py for the CPU baseline. The product
-(naivediffusion_amd) never imports it.
+TEST INFRASTRUCTURE ONLY: imported by tests/ and by __graft_entry__.smoke()
+to check the GPU's results against, and by bench.py for the CPU baseline. The
+product (naivediffusion_amd) never imports it.
 
 Every function takes and returns numpy float32 arrays (int8 / uint16 for
 the quantiser) and names the reference member it follows in oracle.c.

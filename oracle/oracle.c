@@ -4,8 +4,8 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product links or calls this
  * file: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
- * load liboracle.so, and only as the checker (or, for the CPU baseline, as
- * the thing timed beside the GPU). Every function cites the reference
+ * load liboracle.so, and only to check the GPU's results against (or, for
+ * the CPU baseline, as the thing timed beside the GPU). Every function cites the reference
  * member it restates (paths relative to src/NaiveDiffusion/ of the
  * reference). The reference is C#/.NET on DirectML and cannot be built or
  * run here, so nothing is compiled from its sources.

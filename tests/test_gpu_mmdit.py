@@ -106,7 +106,7 @@ def test_config0_block_int8(device, config0):
 
 
 def test_cfg_batch_is_two_single_runs(device):
-    """BASELINE's CFG batch 2 against two batch-1 oracle runs (the
+    """A CFG batch of 2 (cond + uncond) against two batch-1 oracle runs (the
     reference's two sequential Predict calls, GenerationPipeline.cs:592-604)."""
     cfg = C0
     w, xi, xt, temb, cos, sin = block_case(cfg, 256, 64, (16, 16), batch=2, seed=5)
