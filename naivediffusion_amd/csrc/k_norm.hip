@@ -484,7 +484,7 @@ __device__ __forceinline__ float round_t(float v) {
 }
 
 // d = 128 with the element types fixed at compile time (x and y of one type
-// T, the weight of type WT or absent): 8 lanes per (token, head), lane i
+// T, the weight of type WT, or WT = -1 for none): 8 lanes per (token, head), lane i
 // owning the pairs (8i .. 8i+7, 64 + 8i .. 64 + 8i + 7), so every load and
 // store is 16 bytes and no load waits on a type switch. Twice the bandwidth
 // of the 16-lane form on the MMDiT's q and k.
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(256) void head_norm_rotate128_t_kernel(HeadNormRota
   float lo[8], hi[8], wl[8], wh[8];
   load8_t<T>(a.x, xo + i, lo);
   load8_t<T>(a.x, xo + 64 + i, hi);
-  if constexpr (WT != 0) {
+  if constexpr (WT >= 0) {
     load8_t<WT>(a.weight, i, wl);
     load8_t<WT>(a.weight, 64 + i, wh);
   }
@@ -526,8 +526,8 @@ __global__ __launch_bounds__(256) void head_norm_rotate128_t_kernel(HeadNormRota
   float yl[8], yh[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) {
-    const float l = round_t<T>(lo[e] * r * (WT != 0 ? wl[e] : 1.f));
-    const float h = round_t<T>(hi[e] * r * (WT != 0 ? wh[e] : 1.f));
+    const float l = round_t<T>(lo[e] * r * (WT >= 0 ? wl[e] : 1.f));
+    const float h = round_t<T>(hi[e] * r * (WT >= 0 ? wh[e] : 1.f));
     yl[e] = l * cc[e] - h * sv[e];
     yh[e] = h * cc[e] + l * sv[e];
   }
@@ -548,7 +548,7 @@ void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s) {
     const dim3 g((unsigned)((total + 31) / 32));
 #define NDX_HNR(T)                                                                                    \
   do {                                                                                                \
-    if (!a.weight) hipLaunchKernelGGL((head_norm_rotate128_t_kernel<T, 0>), g, dim3(256), 0, s, a);    \
+    if (!a.weight) hipLaunchKernelGGL((head_norm_rotate128_t_kernel<T, -1>), g, dim3(256), 0, s, a);   \
     else if (a.w_dtype == NDX_F32) hipLaunchKernelGGL((head_norm_rotate128_t_kernel<T, NDX_F32>), g, dim3(256), 0, s, a); \
     else hipLaunchKernelGGL((head_norm_rotate128_t_kernel<T, T>), g, dim3(256), 0, s, a);            \
   } while (0)

@@ -666,3 +666,36 @@ def test_elementwise_vector_and_generic_paths(device, dtype):
         err = rel_err(o, e)
         print(f"[gpu]   output {k}: rel err {err:.2e}", flush=True)
         assert err <= tol, (k, err)
+
+
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float16])
+@pytest.mark.parametrize("weight", ["none", "same", "f32"])
+@pytest.mark.parametrize("rotate", [True, False])
+def test_head_norm_rotate_typed_forms(device, dtype, weight, rotate):
+    """The compile-time-typed d = 128 kernel in each of its forms: no
+    weight, a weight of the input's type or fp32, with and without the
+    rotation, against the oracle."""
+    print(f"[gpu] head norm rotate {dtype.name} weight={weight} rotate={rotate}", flush=True)
+    T, H, d = 77, 4, 128
+    x = _round(normal("tx", (1, 1, T, H * d)) * 2, dtype)
+    w = _round(normal("tw", (d,), 0.2) + 1, dtype if weight == "same" else DT.Float32)
+    cos, sin = oracle.mmdit_rope_tables(7, 11, 0)
+    model = nd.ModelBuilder(device, dtype)
+    xi = model.Placeholder([1, 1, T, H * d], dtype)
+    ci = model.Placeholder([1, T, 1, 64], DT.Float32)
+    si = model.Placeholder([1, T, 1, 64], DT.Float32)
+    wi = None
+    if weight == "same":
+        wi = model.Constant(HostTensor.FromFloats(w), [d], dtype)
+    elif weight == "f32":
+        wi = model.Constant(HostTensor.FromFloats(w), [d], DT.Float32)
+    y = Ops.HeadNormRotate(xi, wi, 1e-6, ci if rotate else None, si if rotate else None, H, dtype)
+    model.Compile([y])
+    host_x = HostTensor.FromFloats(x).ConvertTo(dtype)
+    (o,) = run(model, host_x, HostTensor.FromFloats(cos.reshape(1, T, 1, 64)),
+               HostTensor.FromFloats(sin.reshape(1, T, 1, 64)))
+    normed = oracle.rms_norm(x.reshape(T * H, d), w if weight != "none" else np.ones(d, np.float32), 1e-6)
+    ref = normed.reshape(T, H * d)
+    if rotate:
+        ref = oracle.rope(ref, H, cos, sin)
+    assert rel_err(o.reshape(T, -1), ref) <= BF16_TOL
