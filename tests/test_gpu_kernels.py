@@ -188,15 +188,17 @@ def test_int8_linear_against_oracle(device, compute, M):
 
 @pytest.mark.parametrize("tile", ["auto", "256w8lds", "128lds", "64x128lds", "64x64lds", "256"])
 @pytest.mark.parametrize("fmt", ["block32", "channel"])
-def test_int8_kernels_every_tile(device, monkeypatch, tile, fmt):
-    """The int8 GEMMs (direct-to-LDS with the cooperative dequant, and the
-    register-staged one pinned as "256") on ragged shapes, with the
-    reference's block-32 fp16 scales and with per-output-channel fp32 scales
-    (Device.QuantizeInt8 + ModelBuilder.WeightInt8)."""
-    print(f"[gpu] int8 {fmt} tile {tile}", flush=True)
+@pytest.mark.parametrize("K", [1024, 1056])
+def test_int8_kernels_every_tile(device, monkeypatch, tile, fmt, K):
+    """The int8 GEMMs (direct-to-LDS with the pipelined dequant, and the
+    register-staged one pinned as "256") on ragged shapes, K a whole number
+    of 64-wide tiles or ending in half of one, with the reference's block-32
+    fp16 scales and with per-output-channel fp32 scales (Device.QuantizeInt8
+    + ModelBuilder.WeightInt8)."""
+    print(f"[gpu] int8 {fmt} tile {tile} K={K}", flush=True)
     if tile != "auto":
         monkeypatch.setenv("NDX_GEMM_TILE", tile)
-    M, K, N = 700, 1024, 1000
+    M, N = 700, 1000
     x = bf(normal("ix", (1, 1, M, K)))
     w = bf(normal("iw", (N, K), 0.02))
     b = bf(normal("ib", (N,), 0.02))
