@@ -701,3 +701,30 @@ def test_head_norm_rotate_typed_forms(device, dtype, weight, rotate):
     if rotate:
         ref = oracle.rope(ref, H, cos, sin)
     assert rel_err(o.reshape(T, -1), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("d,dtype", [(128, DT.BFloat16), (64, DT.Float16), (128, DT.Float32)])
+@pytest.mark.parametrize("rising", [True, False])
+def test_attention_score_drift(device, d, dtype, rising):
+    """Scores whose scale drifts along the keys (each key row scaled by a ramp
+    from 1 to 12): rising, the running max grows by more than 2^8 many times
+    after the first block and the output is rescaled each time; falling, the
+    max is set early and later probabilities are tiny. Both against the
+    oracle."""
+    print(f"[gpu] attention drift d={d} {dtype.name} rising={rising}", flush=True)
+    T, S, H = 130, 700, 2
+    q = bf(normal("dq", (1, T, H * d)))
+    ramp = np.linspace(1.0, 12.0, S, dtype=np.float32)
+    if not rising:
+        ramp = ramp[::-1].copy()
+    k = bf(normal("dk", (1, S, H * d)) * ramp[None, :, None])
+    v = bf(normal("dv", (1, S, H * d)))
+    model = nd.ModelBuilder(device, dtype)
+    ins = [model.Placeholder([1, 1, n, H * d]) for n in (T, S, S)]
+    model.Compile([Layers.Attend(*ins, H)])
+    host = lambda a: HostTensor.FromFloats(a.reshape(1, 1, -1, H * d))
+    out = run(model, *[host(a) if dtype == DT.Float32 else host(a).ConvertTo(dtype) for a in (q, k, v)])[0]
+    ref = oracle.mha(q, k, v, H)
+    err = rel_err(out.reshape(ref.shape), ref)
+    print(f"[gpu]   rel err {err:.2e}", flush=True)
+    assert err <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
