@@ -728,3 +728,24 @@ def test_attention_score_drift(device, d, dtype, rising):
     err = rel_err(out.reshape(ref.shape), ref)
     print(f"[gpu]   rel err {err:.2e}", flush=True)
     assert err <= (F32_TOL if dtype == DT.Float32 else BF16_TOL)
+
+
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16])
+@pytest.mark.parametrize("D", [512, 640, 1280, 200])
+def test_layer_and_rms_norm_16bit(device, dtype, D):
+    """LayerNorm and RMSNorm on 16-bit rows with 16-bit affine terms (SDXL's
+    640 / 1280 channels; 512 and 1280 take the vectorised kernel, 640 and 200
+    the per-element one), against the oracle on the same rounded inputs."""
+    print(f"[gpu] 16-bit norms {dtype.name} D={D}", flush=True)
+    rows = 37
+    x = _round(normal("n16x", (1, 1, rows, D)) * 2 + 0.5, dtype)
+    w = _round(normal("n16w", (D,), 0.3) + 1, dtype)
+    b = _round(normal("n16b", (D,), 0.3), dtype)
+    model = nd.ModelBuilder(device, dtype)
+    xi = model.Placeholder([1, 1, rows, D], dtype)
+    ln = Layers.LayerNorm(model, xi, HostTensor.FromFloats(w), HostTensor.FromFloats(b), 1e-5)
+    rms = Layers.RmsNorm(model, xi, HostTensor.FromFloats(w), 1e-6)
+    model.Compile([ln, rms])
+    o1, o2 = run(model, HostTensor.FromFloats(x).ConvertTo(dtype))
+    assert rel_err(o1.reshape(rows, D), oracle.layer_norm(x.reshape(rows, D), w, b, 1e-5)) <= BF16_TOL
+    assert rel_err(o2.reshape(rows, D), oracle.rms_norm(x.reshape(rows, D), w, 1e-6)) <= BF16_TOL
