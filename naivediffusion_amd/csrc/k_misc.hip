@@ -134,6 +134,47 @@ __global__ __launch_bounds__(256) void elementwise_vec_kernel(ElemArgs a, int ch
   st8<DT>(a.out, int64_t(c) * 8, z);
 }
 
+// out = in0 (+ in1) where in0 is a token-major [B, H*W, C] tensor viewed as
+// [B, C, H, W] (channel stride 1, pixel stride P) and out and in1 are packed
+// NCHW: SDXL's ToImage(tokens) + x. A workgroup moves a 64-channel x 64-pixel
+// tile through LDS, reading 16 bytes along the channels of each pixel and
+// writing 16 bytes along the pixels of each channel; the generic kernel read
+// the transposed operand one strided element per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_add_kernel(ElemArgs a, int C, int HW, int64_t P) {
+  __shared__ __align__(16) T tile[64][64 + 8];  // [pixel][channel], rows padded by 16 bytes
+  const int tid = threadIdx.x;
+  const int p0 = blockIdx.x * 64, c0 = blockIdx.y * 64, b = blockIdx.z;
+  const T* x = (const T*)a.in0 + b * a.v0.stride[0];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int id = tid + k * 256;        // 512 chunks: 64 pixels x 8 chunks of 8 channels
+    const int px = id >> 3, ch = (id & 7) * 8;
+    *(uint4*)&tile[px][ch] = *(const uint4*)(x + int64_t(p0 + px) * P + c0 + ch);
+  }
+  __syncthreads();
+  const int64_t obase = (int64_t(b) * C + c0) * HW + p0;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int id = tid + k * 256;        // 512 chunks: 64 channels x 8 chunks of 8 pixels
+    const int c = id >> 3, px = (id & 7) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (float)tile[px + e][c];
+    const int64_t o = obase + int64_t(c) * HW + px;
+    if (a.in1) {
+      const uint4 u = *(const uint4*)((const T*)a.in1 + o);
+      const T* y = (const T*)&u;
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] += (float)y[e];
+    }
+    T r[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = (T)v[e];
+    *(uint4*)((T*)a.out + o) = *(const uint4*)r;
+  }
+}
+
 static bool vec_view(const View4& v, bool allow_splat) {
   if (allow_splat && v.stride[3] == 0) return true;  // one scalar load per eight outputs
   if (v.stride[3] != 1) return false;
@@ -159,6 +200,22 @@ void launch_elementwise(const ElemArgs& a, hipStream_t s) {
     if (dt == NDX_F16) hipLaunchKernelGGL((elementwise_vec_kernel<NDX_F16>), g, dim3(256), 0, s, a, chunks);
     else if (dt == NDX_BF16) hipLaunchKernelGGL((elementwise_vec_kernel<NDX_BF16>), g, dim3(256), 0, s, a, chunks);
     else hipLaunchKernelGGL((elementwise_vec_kernel<NDX_F32>), g, dim3(256), 0, s, a, chunks);
+    return;
+  }
+  // The token-major operand of ToImage(tokens) + x.
+  const View4& t = a.v0;
+  const int64_t C = o.size[1], HW = o.size[2] * o.size[3];
+  const bool tr_ok = packed_out && (dt == NDX_F16 || dt == NDX_BF16) && a.dt0 == dt && t.stride[1] == 1 &&
+                     t.stride[3] >= C && t.stride[2] == t.stride[3] * o.size[3] && t.stride[3] % 8 == 0 &&
+                     t.stride[0] % 8 == 0 && C % 64 == 0 && HW % 64 == 0 && (uintptr_t)a.in0 % 16 == 0 &&
+                     (uintptr_t)a.out % 16 == 0 && o.size[0] <= 65535 && C / 64 <= 65535 &&
+                     (a.op == ELEM_COPY || (a.op == ELEM_ADD && a.in1 && a.dt1 == dt && (uintptr_t)a.in1 % 16 == 0 &&
+                                            a.v1.stride[3] == 1 && a.v1.stride[2] == o.size[3] &&
+                                            a.v1.stride[1] == HW && a.v1.stride[0] == C * HW));
+  if (tr_ok && (a.op == ELEM_ADD || !a.in1)) {
+    const dim3 g((unsigned)(HW / 64), (unsigned)(C / 64), (unsigned)o.size[0]);
+    if (dt == NDX_F16) hipLaunchKernelGGL(transpose_add_kernel<_Float16>, g, dim3(256), 0, s, a, (int)C, (int)HW, t.stride[3]);
+    else hipLaunchKernelGGL(transpose_add_kernel<__bf16>, g, dim3(256), 0, s, a, (int)C, (int)HW, t.stride[3]);
     return;
   }
   hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);

@@ -670,6 +670,34 @@ def test_elementwise_vector_and_generic_paths(device, dtype):
         assert err <= tol, (k, err)
 
 
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16, DT.Float32])
+@pytest.mark.parametrize("shape", [(2, 128, 8, 24), (1, 96, 5, 7)])
+def test_to_image_residual(device, dtype, shape):
+    """SDXL's ToImage(tokens) + x (sdxl.py's transformer residual): 16-bit
+    tensors whose channels and pixels are multiples of 64 take the tiled
+    transpose kernel, the rest the generic one; both round the fp32 sum once,
+    so the result equals numpy's bit for bit. ToImage alone (a copy) is checked
+    too."""
+    B, C, H, W = shape
+    print(f"[gpu] ToImage residual {dtype.name} {shape}", flush=True)
+    t_h = _round(normal("ti_t", (B, 1, H * W, C)), dtype)
+    x_h = _round(normal("ti_x", (B, C, H, W)), dtype)
+    g = nd.Graph(device)
+    t = g.Input(dtype, [B, 1, H * W, C])
+    x = g.Input(dtype, [B, C, H, W])
+    img = Layers.ToImage(t, H, W)
+    m = nd.CompiledModel(g, [img + x, Ops.ActivationIdentity(img)], device)
+
+    def host(v):
+        ht = HostTensor.FromFloats(v)
+        return ht if dtype == DT.Float32 else ht.ConvertTo(dtype)
+
+    got = [o.ToFloats().reshape(B, C, H, W) for o in m.Dispatch([host(t_h), host(x_h)])]
+    t_img = t_h.reshape(B, H, W, C).transpose(0, 3, 1, 2)
+    np.testing.assert_array_equal(got[0], _round(t_img + x_h, dtype))
+    np.testing.assert_array_equal(got[1], t_img)
+
+
 @pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float16])
 @pytest.mark.parametrize("weight", ["none", "same", "f32"])
 @pytest.mark.parametrize("rotate", [True, False])
