@@ -1085,6 +1085,20 @@ struct Compiler {
   int pack(int id, std::vector<GNode>& sched) {
     GValue src = values[id];
     int out = new_owner(src.dtype, src.v, src.rank);
+    // The token view [N, 1, P, C] of a packed [N, C, P] buffer (ToTokens of
+    // an NCHW image): the tiled NCHW -> NHWC transposition.
+    const View4& v = src.v;
+    if (dtype_size(src.dtype) == 2 && src.offset == 0 && v.size[1] == 1 && v.stride[2] == 1 &&
+        v.stride[3] == v.size[2] && (v.size[0] == 1 || v.stride[0] == v.size[2] * v.size[3]) && v.size[3] > 1) {
+      GNode t;
+      t.op = OP_NHWC;
+      t.in = {id};
+      t.i1 = 1;
+      t.out = out;
+      t.lane = lane;
+      sched.push_back(t);
+      return out;
+    }
     GNode n;
     n.op = OP_ELEM;
     n.in = {id, NDX_NONE};
@@ -1880,9 +1894,11 @@ struct Runner {
         break;
       }
       case OP_NHWC: {
+        // A packed NCHW value, or (i1) the token view [N, 1, P, C] of one.
         const GValue& x = val(n.in[0]);
-        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], x.v.size[1], x.v.size[2] * x.v.size[3],
-                            s);
+        const int64_t c = n.i1 ? x.v.size[3] : x.v.size[1];
+        const int64_t hw = n.i1 ? x.v.size[2] : x.v.size[2] * x.v.size[3];
+        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], c, hw, s);
         break;
       }
       case OP_UPSAMPLE: {

@@ -98,7 +98,8 @@ __device__ __forceinline__ void st8(void* p, int64_t i, const float (&v)[8]) {
 }
 
 // The elementwise op over eight consecutive innermost elements per thread,
-// every tensor of type DT: the output packed, the first input's innermost
+// every tensor of type DT: the output packed within each index of dimension
+// 0 (a packed tensor or a join's channel slice), the first input's innermost
 // axis contiguous, the second's contiguous or broadcast (stride 0), every
 // row start a multiple of eight elements. Index arithmetic once per eight
 // elements in 32 bits, 16-byte loads and stores, no type switch per load:
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256) void elementwise_vec_kernel(ElemArgs a, int ch
   float z[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) z[e] = apply_elem(a.op, x[e], y[e], a.scale, a.bias);
-  st8<DT>(a.out, int64_t(c) * 8, z);
+  st8<DT>(a.out, offset_of(a.vo, i0, i1, i2, i3), z);
 }
 
 // out = in0 (+ in1) where in0 is a token-major [B, H*W, C] tensor viewed as
@@ -187,12 +188,14 @@ void launch_elementwise(const ElemArgs& a, hipStream_t s) {
   int64_t total = a.vo.size[0] * a.vo.size[1] * a.vo.size[2] * a.vo.size[3];
   if (total == 0) return;
   const View4& o = a.vo;
-  const bool packed_out = o.stride[3] == 1 && o.stride[2] == o.size[3] && o.stride[1] == o.size[2] * o.size[3] &&
-                          o.stride[0] == o.size[1] * o.size[2] * o.size[3];
+  // Rows of the output packed within each index of dimension 0: a packed
+  // tensor, or a join's channel slice of an NCHW one.
+  const bool inner_packed_out = o.stride[3] == 1 && o.stride[2] == o.size[3] && o.stride[1] == o.size[2] * o.size[3];
+  const bool packed_out = inner_packed_out && o.stride[0] == o.size[1] * o.size[2] * o.size[3];
   const int dt = a.dto;
   const int es = dtype_size(dt);
   const bool typed = (dt == NDX_F16 || dt == NDX_BF16 || dt == NDX_F32) && a.dt0 == dt && (!a.in1 || a.dt1 == dt);
-  if (typed && packed_out && o.size[3] % 8 == 0 && total / 8 < (int64_t(1) << 31) && vec_view(a.v0, false) &&
+  if (typed && inner_packed_out && o.stride[0] % 8 == 0 && o.size[3] % 8 == 0 && total / 8 < (int64_t(1) << 31) && vec_view(a.v0, false) &&
       (!a.in1 || vec_view(a.v1, true)) && (uintptr_t)a.out % 16 == 0 && (uintptr_t)a.in0 % 16 == 0 &&
       (!a.in1 || a.v1.stride[3] == 0 || (uintptr_t)a.in1 % 16 == 0) && es > 0) {
     const int chunks = (int)(total / 8);

@@ -698,6 +698,33 @@ def test_to_image_residual(device, dtype, shape):
     np.testing.assert_array_equal(got[1], t_img)
 
 
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16, DT.Float32])
+@pytest.mark.parametrize("shape", [(2, 128, 8, 24), (1, 96, 5, 7), (2, 64, 4, 16)])
+def test_to_tokens_and_channel_join(device, dtype, shape):
+    """SDXL's proj_in input, ToTokens of a computed NCHW image made packed
+    (16-bit channels and pixels multiples of 64: the vectorised NCHW -> NHWC
+    tile; other 16-bit shapes: the scalar tile; fp32: the generic copy), and
+    its up path's channel concatenation (each input written into a channel
+    slice: the vectorised kernel when rows are multiples of 8), both exact."""
+    B, C, H, W = shape
+    print(f"[gpu] ToTokens / channel join {dtype.name} {shape}", flush=True)
+    x_h = _round(normal("tt_x", (B, C, H, W)), dtype)
+    s_h = _round(normal("tt_s", (B, C // 2, H, W)), dtype)
+    g = nd.Graph(device)
+    x = g.Input(dtype, [B, C, H, W])
+    s = g.Input(dtype, [B, C // 2, H, W])
+    img = Ops.ActivationIdentity(x)
+    m = nd.CompiledModel(g, [Layers.ToTokens(img), Ops.Join([img, s], 1)], device)
+
+    def host(v):
+        ht = HostTensor.FromFloats(v)
+        return ht if dtype == DT.Float32 else ht.ConvertTo(dtype)
+
+    tok, cat = (o.ToFloats() for o in m.Dispatch([host(x_h), host(s_h)]))
+    np.testing.assert_array_equal(tok.reshape(B, H * W, C), x_h.reshape(B, C, H * W).transpose(0, 2, 1))
+    np.testing.assert_array_equal(cat.reshape(B, C + C // 2, H, W), np.concatenate([x_h, s_h], 1))
+
+
 @pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float16])
 @pytest.mark.parametrize("weight", ["none", "same", "f32"])
 @pytest.mark.parametrize("rotate", [True, False])
