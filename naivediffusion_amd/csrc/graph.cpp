@@ -1312,6 +1312,24 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     }
   }
 
+  // Rewrite: x * Gelu(y), the GELU's output read by this product only (the
+  // GEGLU of SDXL's feed-forward, Models/Sdxl/UNetLayers.cs), becomes one
+  // elementwise pass; the GELU node is then unreachable and never runs.
+  for (auto& n : src) {
+    if (n.op != OP_ELEM || n.i0 != ELEM_MUL || n.in.size() < 2 || n.in[1] < 0) continue;
+    const int gid = n.in[1];
+    const GValue& gv = c.values[gid];
+    if (gv.kind != VK_NODE || gv.base != gid || gv.producer < 0 || uses[gid] != 1) continue;
+    if (std::find(outs.begin(), outs.end(), gid) != outs.end()) continue;
+    const GNode& p = src[gv.producer];
+    if (p.op != OP_ELEM || p.i0 != ELEM_GELU || p.in.empty() || p.in[0] < 0 ||
+        (p.in.size() > 1 && p.in[1] >= 0) || gv.dtype != c.values[n.out].dtype ||
+        c.values[p.in[0]].dtype != gv.dtype || p.lane != n.lane)
+      continue;
+    n.i0 = ELEM_MUL_GELU;
+    n.in[1] = p.in[0];
+  }
+
   // Reachability from the outputs (through views to their owners).
   std::vector<char> need_node(src.size(), 0);
   std::function<void(int)> mark_value = [&](int id) {

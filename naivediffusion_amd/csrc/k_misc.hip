@@ -27,6 +27,7 @@ __device__ __forceinline__ float apply_elem(int op, float a, float b, float scal
     case ELEM_SUB: return a - b;
     case ELEM_MUL: return a * b;
     case ELEM_DIV: return a / b;
+    case ELEM_MUL_GELU: return a * b;  // b already gelu(y), rounded
     default: return a;
   }
 }
@@ -47,6 +48,7 @@ __global__ void elementwise_kernel(ElemArgs a, int64_t total) {
     int64_t i0 = r / s1;
     float x = load_f(a.in0, a.dt0, offset_of(a.v0, i0, i1, i2, i3));
     float y = a.in1 ? load_f(a.in1, a.dt1, offset_of(a.v1, i0, i1, i2, i3)) : 0.f;
+    if (a.op == ELEM_MUL_GELU) y = round_to(gelu_f(y), a.dto);
     store_f(a.out, a.dto, offset_of(a.vo, i0, i1, i2, i3), apply_elem(a.op, x, y, a.scale, a.bias));
   }
 }
@@ -128,6 +130,10 @@ __global__ __launch_bounds__(256) void elementwise_vec_kernel(ElemArgs a, int ch
     } else {
       ld8<DT>(a.in1, o1, y);
     }
+  }
+  if (a.op == ELEM_MUL_GELU) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = round_to(gelu_f(y[e]), DT);
   }
   float z[8];
 #pragma unroll

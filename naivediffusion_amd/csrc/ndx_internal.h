@@ -166,6 +166,7 @@ enum ElemOp {
   ELEM_SIGMOID, ELEM_SILU, ELEM_GELU, ELEM_TANH, ELEM_GELU_TANH,
   ELEM_SCALE_BIAS,
   ELEM_ADD, ELEM_SUB, ELEM_MUL, ELEM_DIV,
+  ELEM_MUL_GELU,       // x * gelu(y), gelu(y) rounded to the output type first (a GEGLU in one pass)
 };
 struct ElemArgs {
   const void* in0; View4 v0; int dt0;

@@ -671,6 +671,38 @@ def test_elementwise_vector_and_generic_paths(device, dtype):
 
 
 @pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16, DT.Float32])
+@pytest.mark.parametrize("width", [48, 21])
+def test_geglu_fused_equals_unfused(device, dtype, width):
+    """a * Gelu(b) over two halves of one projection (SDXL's GEGLU) runs as
+    one elementwise pass when nothing else reads the GELU; the GELU is still
+    rounded to the compute type before the product, so the fused result
+    equals the two-pass one (the GELU kept as an output) bit for bit, and
+    numpy's within the type's rounding."""
+    B, n = 2, 7
+    print(f"[gpu] GEGLU fused {dtype.name} width {width}", flush=True)
+    p_h = _round(normal("gg", (B, 1, n, 2 * width)), dtype)
+
+    def build(keep_gelu):
+        g = nd.Graph(device)
+        proj = g.Input(dtype, [B, 1, n, 2 * width])
+        gl = Ops.ActivationGelu(Ops.Slice(proj, [0, 0, 0, width], [B, 1, n, width]))
+        y = Ops.Slice(proj, [0, 0, 0, 0], [B, 1, n, width]) * gl
+        m = nd.CompiledModel(g, [y, gl] if keep_gelu else [y], device)
+        m.SetProfiling(True)
+        ht = HostTensor.FromFloats(p_h)
+        out = m.Dispatch([ht if dtype == DT.Float32 else ht.ConvertTo(dtype)])[0].ToFloats()
+        return out, m.Profile()["elementwise"]["launches"]
+
+    fused, n_fused = build(False)
+    split, n_split = build(True)
+    assert (n_fused, n_split) == (1, 2)
+    np.testing.assert_array_equal(fused, split)
+    gelu = lambda v: 0.5 * v * (1.0 + np.vectorize(math.erf)(v / math.sqrt(2.0)))
+    ref = p_h[..., :width] * _round(gelu(p_h[..., width:]), dtype)
+    assert rel_err(fused.reshape(ref.shape), ref) <= (1e-5 if dtype == DT.Float32 else 1.5e-2)
+
+
+@pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16, DT.Float32])
 @pytest.mark.parametrize("shape", [(2, 128, 8, 24), (1, 96, 5, 7)])
 def test_to_image_residual(device, dtype, shape):
     """SDXL's ToImage(tokens) + x (sdxl.py's transformer residual): 16-bit
