@@ -152,18 +152,23 @@ __device__ __forceinline__ void store4(void* p, int dt, int64_t i, float4 v) {
 
 // The same three norms with D = 256 * NC: lane l holds the four-element
 // chunks l, l + 64, ... (NC of them), so every access is a 16- or 8-byte
-// vector and the wave reads one contiguous kilobyte per instruction.
-template <int NC>
+// vector and the wave reads one contiguous kilobyte per instruction. PART:
+// D a multiple of 4 up to 256 * NC (SDXL's 640-wide rows), the chunks past
+// the row neither read nor written.
+template <int NC, bool PART = false>
 __global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const int64_t batch = row / a.rows_per_batch;
   const int64_t xoff = batch * a.batch_x + (row % a.rows_per_batch) * a.ldx;
-  constexpr int D = NC * 256;
+  const int D = PART ? a.D : NC * 256;
   float4 v[NC];
 #pragma unroll
-  for (int j = 0; j < NC; j++) v[j] = load4(a.x, a.x_dtype, xoff + (j * 64 + lane) * 4);
+  for (int j = 0; j < NC; j++) {
+    const int c = (j * 64 + lane) * 4;
+    v[j] = !PART || c < D ? load4(a.x, a.x_dtype, xoff + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   float mean = 0.f;
   if (a.mode != 2) {
     float s = 0.f;
@@ -174,6 +179,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; j++) {
+    if (PART && (j * 64 + lane) * 4 >= D) break;
     const float a0 = v[j].x - mean, a1 = v[j].y - mean, a2 = v[j].z - mean, a3 = v[j].w - mean;
     ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
   }
@@ -183,6 +189,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
 #pragma unroll
   for (int j = 0; j < NC; j++) {
     const int c = (j * 64 + lane) * 4;
+    if (PART && c >= D) break;
     float4 n = make_float4((v[j].x - mean) * rstd, (v[j].y - mean) * rstd, (v[j].z - mean) * rstd,
                            (v[j].w - mean) * rstd);
     if (a.mode == 1) {
@@ -327,6 +334,22 @@ void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
       case 10: hipLaunchKernelGGL(row_norm_vec_kernel<10>, grid, block, 0, s, a); return;
       case 12: hipLaunchKernelGGL(row_norm_vec_kernel<12>, grid, block, 0, s, a); return;
       case 16: hipLaunchKernelGGL(row_norm_vec_kernel<16>, grid, block, 0, s, a); return;
+      default: break;
+    }
+  }
+  const bool part = a.D % 4 == 0 && a.D % 256 != 0 && a.D < 2048 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) &&
+                    vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, 0, a.batch_w) &&
+                    vec_ok(a.bias, a.b_dtype, 0, a.batch_b);
+  if (part) {
+    switch ((a.D + 255) / 256) {
+      case 1: hipLaunchKernelGGL((row_norm_vec_kernel<1, true>), grid, block, 0, s, a); return;
+      case 2: hipLaunchKernelGGL((row_norm_vec_kernel<2, true>), grid, block, 0, s, a); return;
+      case 3: hipLaunchKernelGGL((row_norm_vec_kernel<3, true>), grid, block, 0, s, a); return;
+      case 4: hipLaunchKernelGGL((row_norm_vec_kernel<4, true>), grid, block, 0, s, a); return;
+      case 5: hipLaunchKernelGGL((row_norm_vec_kernel<5, true>), grid, block, 0, s, a); return;
+      case 6: hipLaunchKernelGGL((row_norm_vec_kernel<6, true>), grid, block, 0, s, a); return;
+      case 7: hipLaunchKernelGGL((row_norm_vec_kernel<7, true>), grid, block, 0, s, a); return;
+      case 8: hipLaunchKernelGGL((row_norm_vec_kernel<8, true>), grid, block, 0, s, a); return;
       default: break;
     }
   }

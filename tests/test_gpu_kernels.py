@@ -818,11 +818,12 @@ def test_attention_score_drift(device, d, dtype, rising):
 
 
 @pytest.mark.parametrize("dtype", [DT.Float16, DT.BFloat16])
-@pytest.mark.parametrize("D", [512, 640, 1280, 200])
+@pytest.mark.parametrize("D", [512, 640, 1280, 200, 202])
 def test_layer_and_rms_norm_16bit(device, dtype, D):
     """LayerNorm and RMSNorm on 16-bit rows with 16-bit affine terms (SDXL's
     640 / 1280 channels; 512 and 1280 take the vectorised kernel, 640 and 200
-    the per-element one), against the oracle on the same rounded inputs."""
+    its form for widths that are a multiple of 4 but not of 256, 202 the
+    per-element one), against the oracle on the same rounded inputs."""
     print(f"[gpu] 16-bit norms {dtype.name} D={D}", flush=True)
     rows = 37
     x = _round(normal("n16x", (1, 1, rows, D)) * 2 + 0.5, dtype)
