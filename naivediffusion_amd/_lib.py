@@ -133,8 +133,23 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        _check_fresh(L)
         _lib = L
     return _lib
+
+
+def _check_fresh(L) -> None:
+    """Refuses a library built from sources other than the ones beside it:
+    ndx_version() ends with the hash build.py embeds."""
+    from .build import CSRC, source_hash
+    if not CSRC.is_dir():
+        return  # an installed library without its sources: nothing to compare
+    built = L.ndx_version().decode().rsplit(" ", 1)[-1]
+    want = source_hash()
+    if built != want:
+        raise ImportError(
+            f"{LIB_PATH} is stale: built from sources with hash {built}, the sources here hash to {want}. "
+            "Rebuild it (python -m naivediffusion_amd.build).")
 
 
 def check(status: int) -> None:

@@ -9,6 +9,7 @@ repository snapshot to the machine that runs it. Run as
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -37,6 +38,23 @@ HIPCC_FLAGS = [
 ]
 
 
+def source_hash() -> str:
+    """SHA-256 (first 16 hex digits) of every source the library is built
+    from and the flags it is built with. The build embeds it in
+    ndx_version(); the loader compares it with the sources beside the
+    library and refuses a library built from other sources."""
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(CSRC.glob("*.h"))
+    files.append(PACKAGE.parent / "include" / "ndx.h")
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def _hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if candidate and Path(candidate).exists():
@@ -44,9 +62,9 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library cannot be built")
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, digest: str) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, f'-DNDX_SOURCE_HASH="{digest}"', "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd.insert(1, "-xhip")
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -64,8 +82,9 @@ def _compile(src: Path) -> Path:
 def build(verbose: bool = True) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+    digest = source_hash()
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as pool:
-        objects = list(pool.map(_compile, sources))
+        objects = list(pool.map(lambda src: _compile(src, digest), sources))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -73,7 +92,7 @@ def build(verbose: bool = True) -> Path:
         raise RuntimeError(f"linking libndx.so failed:\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
     if verbose:
-        print(f"built {LIBRARY} from {len(sources)} sources")
+        print(f"built {LIBRARY} from {len(sources)} sources (source hash {digest})")
     return LIBRARY
 
 

@@ -239,7 +239,12 @@ static void mark_lost_on(ndx_device* dev, const ndx::Error& e) {
 extern "C" {
 
 NDX_API const char* ndx_last_error(void) { return g_last_error.c_str(); }
-NDX_API const char* ndx_version(void) { return "ndx 0.1 (gfx950)"; }
+#ifndef NDX_SOURCE_HASH
+#define NDX_SOURCE_HASH "unknown"
+#endif
+// The last word is the hash of the sources the library was built from
+// (naivediffusion_amd/build.py); the Python loader refuses a mismatch.
+NDX_API const char* ndx_version(void) { return "ndx 0.2 (gfx950) src " NDX_SOURCE_HASH; }
 
 NDX_API ndx_status ndx_device_count(int32_t* count) {
   NDX_TRY

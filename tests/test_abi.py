@@ -48,6 +48,17 @@ def test_version_and_device_count_without_a_gpu():
     assert nd.Device.Count() >= 0
 
 
+def test_the_library_was_built_from_these_sources():
+    """ndx_version() ends with the hash of the sources the library was built
+    from; the loader refuses a library whose hash is not the sources' now."""
+    from naivediffusion_amd import build
+    built = _lib.lib().ndx_version().decode().rsplit(" ", 1)[-1]
+    assert built == build.source_hash()
+    fake = type("L", (), {"ndx_version": staticmethod(lambda: b"ndx 0.2 (gfx950) src 0123456789abcdef")})
+    with pytest.raises(ImportError, match="stale"):
+        _lib._check_fresh(fake)
+
+
 def test_host_quantizer_is_bit_exact_with_golden_and_oracle():
     g = np.load(GOLDEN)
     for name in ("mixed", "zero", "ties", "big", "small"):

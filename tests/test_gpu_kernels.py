@@ -519,6 +519,31 @@ def test_errors_leave_the_device_usable(device):
         model.Compiled.DispatchOnDevice([device.Upload(HostTensor.FromFloats(np.zeros(3, np.float32)))])
 
 
+def test_device_lost_is_fatal_to_that_device_only(device):
+    """DeviceRemovedException (Dml/DmlDevice.cs:948-953): once a device
+    reports itself lost, every call on it fails with DeviceRemovedError
+    (uploads, runs of a model compiled before, new graphs), while another
+    device on the same GPU keeps working. Forced from the host on a second
+    device: no GPU fault."""
+    other = nd.Device()
+    model = nd.ModelBuilder(other)
+    x = model.Placeholder([1, 1, 2, 2])
+    model.Compile([x * 2.0])
+    inp = HostTensor.FromFloats(np.ones(4, np.float32), 1, 1, 2, 2)
+    assert np.array_equal(model.Run(inp)[0].ToFloats().ravel(), np.full(4, 2, np.float32))
+    other.SetFaultInjection(2)
+    with pytest.raises(nd.DeviceRemovedError):
+        other.Upload(HostTensor.FromFloats(np.zeros(4, np.float32)))
+    with pytest.raises(nd.DeviceRemovedError):
+        model.Run(inp)
+    with pytest.raises(nd.DeviceRemovedError):
+        other.Empty(DT.Float32, [16])
+    model.Dispose()
+    other.Dispose()
+    t = device.Upload(HostTensor.FromFloats(np.arange(4, dtype=np.float32)))
+    assert np.array_equal(t.Download().ToFloats(), np.arange(4, dtype=np.float32))
+
+
 @pytest.mark.parametrize("shape,groups", [((2, 320, 64, 64), 32), ((2, 1920, 32, 32), 32), ((1, 64, 7, 9), 32),
                                           ((2, 640, 33, 31), 32), ((1, 32, 256, 256), 4)])
 @pytest.mark.parametrize("dtype,silu", [(DT.Float16, True), (DT.BFloat16, False), (DT.Float32, True)])
