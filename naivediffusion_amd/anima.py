@@ -118,14 +118,18 @@ def synthetic_weights(cfg: AnimaConfig, seed: int, names=None, norm_spread: floa
 
 
 def device_weights(device: Device, cfg: AnimaConfig, seed: int, dtype: HostDataType = HostDataType.BFloat16,
-                   names=None) -> Dict[str, DeviceTensor]:
-    """The synthetic weights made on the GPU at `dtype` (norm weights 1)."""
+                   names=None, norm_spread: float = 0.0) -> Dict[str, DeviceTensor]:
+    """The synthetic weights made on the GPU at `dtype` (norm weights 1, +
+    N(0, norm_spread) made on the host as synthetic_weights makes them)."""
     shapes = weight_shapes(cfg)
     out = {}
     for name in (names or shapes):
         shape = shapes[name]
         if _is_norm(name):
-            out[name] = device.Upload(HostTensor.FromFloats(np.ones(shape, np.float32)).ConvertTo(dtype))
+            v = np.ones(shape, np.float32)
+            if norm_spread:
+                v = v + rng.normal(rng.tensor_seed(seed, name), shape, 0.0, norm_spread)
+            out[name] = device.Upload(HostTensor.FromFloats(v).ConvertTo(dtype))
         else:
             out[name] = device.Normal(dtype, shape, rng.tensor_seed(seed, name), 0.0, 0.02)
     return out

@@ -108,16 +108,20 @@ def synthetic_weights(cfg: MmditConfig, seed: int, names=None, norm_spread: floa
     return out
 
 
-def device_weights(device: Device, cfg: MmditConfig, seed: int, names=None) -> Dict[str, DeviceTensor]:
-    """The same weights made on the GPU in bf16 (norm weights 1): the
+def device_weights(device: Device, cfg: MmditConfig, seed: int, names=None,
+                   norm_spread: float = 0.0) -> Dict[str, DeviceTensor]:
+    """The same weights made on the GPU in bf16 (norm weights 1, + N(0,
+    norm_spread) made on the host as synthetic_weights makes them): the
     synthetic model of the benchmark, never passing through host memory."""
     shapes = weight_shapes(cfg)
     out = {}
     for name in (names or shapes):
         shape = shapes[name]
         if _is_norm(name):
-            out[name] = device.Upload(HostTensor(HostDataType.BFloat16, shape,
-                                                 f32_to_bf16(np.ones(shape, np.float32))))
+            v = np.ones(shape, np.float32)
+            if norm_spread:
+                v = v + rng.normal(rng.tensor_seed(seed, name), shape, 0.0, norm_spread)
+            out[name] = device.Upload(HostTensor(HostDataType.BFloat16, shape, f32_to_bf16(v)))
         else:
             out[name] = device.Normal(HostDataType.BFloat16, shape, rng.tensor_seed(seed, name), 0.0, 0.02)
     return out
@@ -244,15 +248,17 @@ def build_block(model: ModelBuilder, W: _W, i: int, cfg: MmditConfig, x_img, x_t
 
 
 def build_block_model(device: Device, cfg: MmditConfig, weights: dict, batch: int, n_img: int, n_txt: int,
-                      compute: HostDataType, int8: bool = False, block: int = 0, key_len: bool = False,
+                      compute: HostDataType, int8=False, block: int = 0, key_len: bool = False,
                       two_streams: bool = True):
     """A compiled single-block model. Inputs in order: x_img [B,1,Ni,D],
     x_txt [B,1,Nt,D], temb [B,1,1,D] (the time embedding before SiLU), cos,
     sin [1,N,1,64] (and the key length [1,1,1,1] when key_len). Outputs the
-    updated x_img, x_txt (fp32)."""
+    updated x_img, x_txt (fp32). int8 as in build_step_model ("channel"
+    needs the weights as device tensors)."""
     D = cfg.width
-    model = ModelBuilder(device, compute, int8)
-    W = _W(model, weights, compute)
+    per_channel = int8 == "channel"
+    model = ModelBuilder(device, compute, bool(int8) and not per_channel)
+    W = _W(model, weights, compute, per_channel)
     xi = model.Placeholder([batch, 1, n_img, D], HostDataType.Float32)
     xt = model.Placeholder([batch, 1, n_txt, D], HostDataType.Float32)
     temb = model.Placeholder([batch, 1, 1, D], HostDataType.Float32)
