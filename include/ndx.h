@@ -320,6 +320,22 @@ NDX_API ndx_status ndx_model_run(ndx_model* model, ndx_tensor* const* inputs, in
 NDX_API ndx_status ndx_model_run_into_async(ndx_model* model, ndx_tensor* const* inputs,
                                             int32_t n_inputs, ndx_tensor* const* outputs,
                                             int32_t n_outputs);
+/* No counterpart in the reference: ndx_model_run_into_async for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The model's temporary memory (every
+ * intermediate and the kernels' scratch: attention key-split partials,
+ * GroupNorm split statistics) lives in a static array the library holds on
+ * each GPU until the process ends, 64 MiB (NDX_STATIC_SCRATCH_BYTES), instead
+ * of the model's own arena; the call allocates nothing and records no timing
+ * events. A model whose temporary size (ndx_model_sizes) exceeds the array
+ * is refused with NDX_INVALID_ARG. Every static run on a GPU shares that
+ * GPU's array: runs queued on one device handle are ordered by its stream,
+ * but runs that overlap on one GPU (two device handles, or other streams)
+ * race. */
+#define NDX_STATIC_SCRATCH_BYTES (64ull << 20)
+NDX_API ndx_status ndx_model_run_into_static_async(ndx_model* model, ndx_tensor* const* inputs,
+                                                   int32_t n_inputs, ndx_tensor* const* outputs,
+                                                   int32_t n_outputs);
 /* Kernel timing with no reference counterpart: while enabled, every kernel a
  * run launches is bracketed by HIP events on the device stream. */
 NDX_API ndx_status ndx_model_set_profiling(ndx_model* model, int32_t enabled);

@@ -1253,6 +1253,8 @@ static void plan_lanes(ndx_model* m, const std::vector<int>& last) {
     for (int t = 0; t < 2; t++)
       if (m->waits[i][t] >= 0 && m->signal[m->waits[i][t]] < 0) m->signal[m->waits[i][t]] = ne++;
   m->lane_events.resize(ne + 2);
+  // The second stream exists before the first run, so no run creates it.
+  (void)m->dev->aux_stream();
   // Both lanes are on this device: a device-scope release makes a lane's
   // writes visible to the other (all XCDs), without the system-scope cache
   // writeback a default event does.
@@ -1555,11 +1557,11 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       }
       if (node.scratch_bytes > 0) node.scratch_off = place(node.scratch_bytes, i);
     }
+    // The arena (the reference's temporary resource) is allocated by the
+    // first run that uses it, as DmlDevice sizes its temporary buffer at
+    // dispatch; a model run only through ndx_model_run_into_static_async
+    // never allocates one.
     m->arena_bytes = (size_t)top;
-    if (top > 0) {
-      m->arena_alloc = pool_round(m->arena_bytes);
-      m->arena = m->dev->alloc(m->arena_alloc);
-    }
     plan_lanes(m, last);
     for (auto& n : m->nodes) m->kernels += (n.op == OP_JOIN) ? (int)n.in.size() : 1;
   } catch (...) {
@@ -1578,6 +1580,7 @@ struct Runner {
   ndx_model* m;
   ndx_tensor* const* in;
   std::vector<void*> out_ptr;
+  char* arena = nullptr;  // the temporary memory of this run
 
   char* base_ptr(int base) {
     const GValue& b = m->values[base];
@@ -1586,7 +1589,7 @@ struct Runner {
       case VK_CONST: return (char*)b.data->ptr;
       default:
         if (m->out_slot[base] >= 0) return (char*)out_ptr[m->out_slot[base]];
-        return (char*)m->arena + m->arena_off[base];
+        return arena + m->arena_off[base];
     }
   }
   void* ptr(int id) {
@@ -1783,7 +1786,7 @@ struct Runner {
           // [b, h, t, s] strides; a size-1 axis broadcasts.
           for (int i = 0; i < 4; i++) a.mask_stride[i] = mk.v.size[i] == 1 ? 0 : mk.v.stride[i];
         }
-        launch_attention(a, n.scratch_bytes > 0 ? (char*)m->arena + n.scratch_off : nullptr, s);
+        launch_attention(a, n.scratch_bytes > 0 ? arena + n.scratch_off : nullptr, s);
         break;
       }
       case OP_HNR: {
@@ -1867,7 +1870,7 @@ struct Runner {
           a.bias = ptr(n.in[2]);
           a.w_dtype = val(n.in[2]).dtype;
         }
-        a.partial = (float*)((char*)m->arena + n.scratch_off);
+        a.partial = (float*)(arena + n.scratch_off);
         a.splits = group_norm_splits(int64_t(a.C / a.groups) * a.HW);
         launch_group_norm(a, s);
         break;
@@ -1970,7 +1973,31 @@ void check_inputs(ndx_model* m, ndx_tensor* const* inputs, int32_t n_inputs) {
   }
 }
 
-void run_nodes(ndx_model* m, Runner& r) {
+// The model's own arena, allocated by its first run.
+char* model_arena(ndx_model* m) {
+  if (!m->arena && m->arena_bytes > 0) {
+    m->arena_alloc = pool_round(m->arena_bytes);
+    m->arena = m->dev->alloc(m->arena_alloc);
+  }
+  return (char*)m->arena;
+}
+
+// Checks the caller's output tensors and records their pointers.
+void bind_outputs(ndx_model* m, Runner& r, ndx_tensor* const* outputs, int32_t n_outputs) {
+  if (!outputs) fail(NDX_INVALID_ARG, "outputs is null");
+  if (n_outputs != (int)m->outputs.size()) fail(NDX_INVALID_ARG, "wrong number of outputs");
+  for (int k = 0; k < n_outputs; k++) {
+    const GValue& v = m->values[m->outputs[k]];
+    ndx_tensor* t = outputs[k];
+    if (!t || t->dtype != v.dtype || t->numel() != numel4(v.v) || t->dev != m->dev)
+      fail(NDX_INVALID_ARG, "output " + std::to_string(k) + " is not " + shape_str(v.v, v.dtype));
+    r.out_ptr.push_back(t->ptr);
+  }
+}
+
+// Queues every node. With profile false no timing events are recorded (and
+// none created), whatever the model's profiling setting.
+void run_nodes(ndx_model* m, Runner& r, bool profile = true) {
   hipStream_t s = m->dev->stream;
   hipStream_t st[2] = {s, m->two_lanes ? m->dev->aux_stream() : s};
   const int ne = (int)m->lane_events.size();
@@ -1980,8 +2007,8 @@ void run_nodes(ndx_model* m, Runner& r) {
     hip_check(hipEventRecord(m->lane_events[ne - 2], s), "hipEventRecord");
     hip_check(hipStreamWaitEvent(st[1], m->lane_events[ne - 2], 0), "hipStreamWaitEvent");
   }
-  const bool filtered = m->profiling && !m->prof_filter.empty();
-  const bool full = m->profiling && !filtered;
+  const bool filtered = profile && m->profiling && !m->prof_filter.empty();
+  const bool full = profile && m->profiling && !filtered;
   size_t need = m->nodes.size() * 2;
   while (full && m->events.size() < need) {
     hipEvent_t e;
@@ -2125,6 +2152,7 @@ NDX_API ndx_status ndx_model_run(ndx_model* m, ndx_tensor* const* inputs, int32_
     if (n_outputs != (int)m->outputs.size())
       fail(NDX_INVALID_ARG, "the model has " + std::to_string(m->outputs.size()) + " outputs, not " + std::to_string(n_outputs));
     Runner r{m, inputs, {}};
+    r.arena = model_arena(m);
     for (int id : m->outputs) {
       const GValue& v = m->values[id];
       int64_t shape[4];
@@ -2156,16 +2184,42 @@ NDX_API ndx_status ndx_model_run_into_async(ndx_model* m, ndx_tensor* const* inp
     if (n_inputs > 0 && !inputs) fail(NDX_INVALID_ARG, "inputs is null");
     if (!outputs) fail(NDX_INVALID_ARG, "outputs is null");
     check_inputs(m, inputs, n_inputs);
-    if (n_outputs != (int)m->outputs.size()) fail(NDX_INVALID_ARG, "wrong number of outputs");
     Runner r{m, inputs, {}};
-    for (int k = 0; k < n_outputs; k++) {
-      const GValue& v = m->values[m->outputs[k]];
-      ndx_tensor* t = outputs[k];
-      if (!t || t->dtype != v.dtype || t->numel() != numel4(v.v) || t->dev != m->dev)
-        fail(NDX_INVALID_ARG, "output " + std::to_string(k) + " is not " + shape_str(v.v, v.dtype));
-      r.out_ptr.push_back(t->ptr);
-    }
+    bind_outputs(m, r, outputs, n_outputs);
+    r.arena = model_arena(m);
     run_nodes(m, r);
+  } catch (const ndx::Error& e) {
+    if (e.status == NDX_DEVICE_LOST) m->dev->lost = true;
+    set_last_error(e.message);
+    return e.status;
+  }
+  return NDX_OK;
+}
+
+NDX_API ndx_status ndx_model_run_into_static_async(ndx_model* m, ndx_tensor* const* inputs, int32_t n_inputs,
+                                                   ndx_tensor* const* outputs, int32_t n_outputs) {
+  if (!m) {
+    set_last_error("model is null");
+    return NDX_INVALID_ARG;
+  }
+  try {
+    m->dev->check_usable();
+    if (n_inputs > 0 && !inputs) fail(NDX_INVALID_ARG, "inputs is null");
+    check_inputs(m, inputs, n_inputs);
+    Runner r{m, inputs, {}};
+    bind_outputs(m, r, outputs, n_outputs);
+    if (m->arena_bytes > kStaticScratchBytes)
+      fail(NDX_INVALID_ARG, "the model needs " + std::to_string(m->arena_bytes) +
+                                " bytes of temporary memory; the static scratch holds " +
+                                std::to_string(kStaticScratchBytes));
+    if (!m->dev->static_scratch)
+      fail(NDX_UNSUPPORTED, "the static scratch is not available on this device (" +
+                                m->dev->static_scratch_error + ")");
+    // Every intermediate and every kernel's scratch (attention key-split
+    // partials, GroupNorm split statistics) is written before it is read
+    // within one run, so nothing left by an earlier run needs clearing.
+    r.arena = (char*)m->dev->static_scratch;
+    run_nodes(m, r, false);
   } catch (const ndx::Error& e) {
     if (e.status == NDX_DEVICE_LOST) m->dev->lost = true;
     set_last_error(e.message);

@@ -259,6 +259,27 @@ NDX_API ndx_status ndx_device_count(int32_t* count) {
   NDX_CATCH
 }
 
+// The temporary memory of ndx_model_run_into_static_async: every GPU the
+// library runs on holds its own copy from the library's load until the
+// process ends, and every static run on that GPU shares it. In host code the
+// name `scratch` is a host-side stand-in, not a device address: the address
+// is looked up once per device below (hipGetSymbolAddress, with the device
+// current) and only that address, ndx_device::static_scratch, is used.
+static __device__ __align__(256) char scratch[ndx::kStaticScratchBytes];
+
+// Looks up this GPU's copy of the static scratch array; a failure is kept
+// and reported by the static run, not by the device creation.
+static void find_static_scratch(ndx_device* dev) {
+  void* p = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || !p) {
+    (void)hipGetLastError();
+    dev->static_scratch_error = std::string("hipGetSymbolAddress: ") + hipGetErrorString(err);
+    return;
+  }
+  dev->static_scratch = p;
+}
+
 NDX_API ndx_status ndx_device_create(int32_t adapter, ndx_device** out) {
   NDX_TRY
   if (!out) fail(NDX_INVALID_ARG, "out is null");
@@ -285,6 +306,7 @@ NDX_API ndx_status ndx_device_create(int32_t adapter, ndx_device** out) {
     delete dev;
     hip_check(err, "hipStreamCreate");
   }
+  find_static_scratch(dev);
   *out = dev;
   NDX_CATCH
 }

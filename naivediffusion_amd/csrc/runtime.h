@@ -8,15 +8,25 @@
 
 #include "ndx_internal.h"
 
+namespace ndx {
+// Bytes of the static scratch array that ndx_model_run_into_static_async
+// uses as a model's temporary memory (one array per GPU, process lifetime).
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+}  // namespace ndx
+
 struct ndx_device {
   int id = 0;
   hipStream_t stream = nullptr;
-  hipStream_t aux = nullptr;  // the second lane of a compiled model, made on first use
+  hipStream_t aux = nullptr;  // the second lane, made when a two-lane model is compiled
   std::string name;
   bool lost = false;
   bool destroyed = false;  // ndx_device_destroy ran; freed when refs drops to 0
   int64_t refs = 0;        // live tensors and model arenas allocated here
   int fault = 0;           // ndx_device_set_fault_injection kind
+  // Device address of the static scratch array on this GPU (looked up when
+  // the device is created), or null with the reason in static_scratch_error.
+  void* static_scratch = nullptr;
+  std::string static_scratch_error;
 
   // Caching pool: freed blocks are kept by rounded size and handed out
   // again, the way DmlBufferPool recycles committed resources.

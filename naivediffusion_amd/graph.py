@@ -325,6 +325,9 @@ class CompiledModel:
     """A compiled graph with its weights on the device (DmlCompiledModel,
     Dml/DmlCompiledModel.cs:10)."""
 
+    # The static scratch of DispatchIntoStatic (NDX_STATIC_SCRATCH_BYTES).
+    STATIC_SCRATCH_BYTES = 64 << 20
+
     def __init__(self, graph: Graph, outputs: Sequence[Expression], device: Device):
         if graph.handle is None:
             raise InvalidOperationError("the graph was disposed")
@@ -367,6 +370,14 @@ class CompiledModel:
         arr = (ctypes.c_void_p * max(len(inputs), 1))(*[t.handle for t in inputs])
         outs = (ctypes.c_void_p * len(outputs))(*[t.handle for t in outputs])
         call("ndx_model_run_into_async", self.handle, arr, len(inputs), outs, len(outputs))
+
+    def DispatchIntoStatic(self, inputs: Sequence[DeviceTensor], outputs: Sequence[DeviceTensor]) -> None:
+        """DispatchInto with the temporaries in the library's static scratch
+        (ndx_model_run_into_static_async): allocates nothing; refuses a model
+        whose TemporarySize exceeds STATIC_SCRATCH_BYTES."""
+        arr = (ctypes.c_void_p * max(len(inputs), 1))(*[t.handle for t in inputs])
+        outs = (ctypes.c_void_p * len(outputs))(*[t.handle for t in outputs])
+        call("ndx_model_run_into_static_async", self.handle, arr, len(inputs), outs, len(outputs))
 
     def Dispatch(self, inputs: Sequence[HostTensor]) -> list[HostTensor]:
         device_in = [self.Device.Upload(t) for t in inputs]
