@@ -1528,40 +1528,59 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       int64_t off, size;
       int last;
     };
-    std::vector<Live> live;
-    int64_t top = 0;
-    // First fit of [size] bytes among the live ranges; returns the offset.
-    auto place = [&](int64_t bytes, int until) {
+    // Each lane gets a region of its own: a value never takes bytes that a
+    // value of the other lane held, so freeing memory never makes one
+    // stream wait for the other (only data does). Lane 1's region follows
+    // lane 0's.
+    std::vector<Live> live[2];
+    int64_t top[2] = {0, 0};
+    std::vector<int8_t> region(nv, 0);
+    std::vector<int8_t> scratch_region(m->nodes.size(), 0);
+    // First fit of [size] bytes among the region's live ranges; returns the offset.
+    auto place = [&](int r, int64_t bytes, int until) {
       int64_t size = (bytes + 255) & ~int64_t(255);
-      std::sort(live.begin(), live.end(), [](const Live& a, const Live& b) { return a.off < b.off; });
+      auto& lv = live[r];
+      std::sort(lv.begin(), lv.end(), [](const Live& a, const Live& b) { return a.off < b.off; });
       int64_t off = 0;
-      for (const Live& l : live) {
+      for (const Live& l : lv) {
         if (off + size <= l.off) break;
         off = std::max(off, l.off + l.size);
       }
-      live.push_back({off, size, until});
-      top = std::max(top, off + size);
+      lv.push_back({off, size, until});
+      top[r] = std::max(top[r], off + size);
       return off;
     };
     for (int i = 0; i < (int)m->nodes.size(); i++) {
       GNode& node = m->nodes[i];
-      live.erase(std::remove_if(live.begin(), live.end(), [&](const Live& l) { return l.last < i; }), live.end());
+      for (auto& lv : live)
+        lv.erase(std::remove_if(lv.begin(), lv.end(), [&](const Live& l) { return l.last < i; }), lv.end());
       // The second of a paired linear is written by the first's launch: its
       // output is placed (and live) from there.
       if (node.op == OP_LINEAR && node.i5 == 2) continue;
+      const int r = node.lane & 1;
       for (int k = 0; k < (node.op == OP_LINEAR && node.i5 == 1 ? 2 : 1); k++) {
         const int id = m->nodes[i + k].out;
-        if (m->out_slot[id] < 0)
+        if (m->out_slot[id] < 0) {
           m->arena_off[id] =
-              place(int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype), std::max(last[id], i + k));
+              place(r, int64_t(m->values[id].buffer_elems) * dtype_size(m->values[id].dtype), std::max(last[id], i + k));
+          region[id] = (int8_t)r;
+        }
       }
-      if (node.scratch_bytes > 0) node.scratch_off = place(node.scratch_bytes, i);
+      if (node.scratch_bytes > 0) {
+        node.scratch_off = place(r, node.scratch_bytes, i);
+        scratch_region[i] = (int8_t)r;
+      }
     }
+    const int64_t base1 = (top[0] + 255) & ~int64_t(255);
+    for (int id = 0; id < nv; id++)
+      if (m->arena_off[id] >= 0 && region[id] == 1) m->arena_off[id] += base1;
+    for (size_t i = 0; i < m->nodes.size(); i++)
+      if (m->nodes[i].scratch_bytes > 0 && scratch_region[i] == 1) m->nodes[i].scratch_off += base1;
     // The arena (the reference's temporary resource) is allocated by the
     // first run that uses it, as DmlDevice sizes its temporary buffer at
     // dispatch; a model run only through ndx_model_run_into_static_async
     // never allocates one.
-    m->arena_bytes = (size_t)top;
+    m->arena_bytes = (size_t)(top[1] > 0 ? base1 + top[1] : top[0]);
     plan_lanes(m, last);
     for (auto& n : m->nodes) m->kernels += (n.op == OP_JOIN) ? (int)n.in.size() : 1;
   } catch (...) {
