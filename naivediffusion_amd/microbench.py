@@ -7,7 +7,9 @@ its own, so their rates can be read apart from the step's two streams:
 - adaln_gemv: the per-block adaLN projection, SiLU(temb) [1, 3072] times
   [18432, 3072] bf16 plus an fp32 bias (M = 1: a weight-streaming GEMV);
 - head_norm_rotate: the per-head RMSNorm + fp32 RoPE of Q read out of the
-  packed QKV projection.
+  packed QKV projection;
+- gemm_qkv / gemm_out / gemm_fc1 / gemm_fc2: the image stream's four
+  projections alone (rates in TFLOP/s).
 
 Every launch is bracketed by HIP events on the stream it runs on; the
 printed rate is the algorithmic bytes per launch over the mean launch time.
@@ -69,12 +71,28 @@ def _head_norm_rotate(dev, rows):
     return CompiledModel(g, [out], dev), ins, rows * D * 2 * 2 + rows * 64 * 4 * 2
 
 
+def _gemm(dev, M, N, K):
+    """One image-stream projection: x [M, K] bf16 times W [N, K] bf16."""
+    from .graph import ModelBuilder
+    m = ModelBuilder(dev, DT.BFloat16)
+    x = m.Placeholder([1, 1, M, K], DT.BFloat16)
+    w = m.WeightOnDevice(dev.Normal(DT.BFloat16, [N, K], 7, 0.0, 0.02), N)
+    m.Compile([Layers.Linear(m, x, w)])
+    return m.Compiled, [dev.Normal(DT.BFloat16, [1, 1, M, K], 8)], 2.0 * M * N * K
+
+
 CASES = {
     "modulate_img": lambda dev: _modulate(dev, NI),
     "modulate_txt": lambda dev: _modulate(dev, NT),
     "adaln_gemv": _adaln_gemv,
     "head_norm_rotate_img": lambda dev: _head_norm_rotate(dev, NI),
+    # the image stream's four products (flops, not bytes, per launch)
+    "gemm_qkv": lambda dev: _gemm(dev, NI, 3 * D, D),
+    "gemm_out": lambda dev: _gemm(dev, NI, D, D),
+    "gemm_fc1": lambda dev: _gemm(dev, NI, 4 * D, D),
+    "gemm_fc2": lambda dev: _gemm(dev, NI, D, 4 * D),
 }
+FLOP_CASES = {"gemm_qkv", "gemm_out", "gemm_fc1", "gemm_fc2"}
 
 
 def run(ops, reps: int = 50, warmup: int = 5):
@@ -93,10 +111,16 @@ def run(ops, reps: int = 50, warmup: int = 5):
             compiled.SetProfiling(False)
             fam, e = max(prof.items(), key=lambda kv: kv[1]["ms"])
             us = e["ms"] / e["launches"] * 1e3
-            results[name] = {"kernel": fam, "us_per_launch": us, "bytes_per_launch": nbytes,
-                             "GB_per_s": nbytes / (us * 1e-6) / 1e9, "launches": e["launches"]}
-            print(f"{name:22s} {fam:34s} {us:9.2f} us {nbytes / 1e6:9.2f} MB "
-                  f"{nbytes / (us * 1e-6) / 1e9:8.1f} GB/s", flush=True)
+            if name in FLOP_CASES:
+                results[name] = {"kernel": fam, "us_per_launch": us, "flop_per_launch": nbytes,
+                                 "TFLOP_per_s": nbytes / (us * 1e-6) / 1e12, "launches": e["launches"]}
+                print(f"{name:22s} {fam:34s} {us:9.2f} us {nbytes / 1e9:9.2f} GF "
+                      f"{nbytes / (us * 1e-6) / 1e12:8.1f} TFLOP/s", flush=True)
+            else:
+                results[name] = {"kernel": fam, "us_per_launch": us, "bytes_per_launch": nbytes,
+                                 "GB_per_s": nbytes / (us * 1e-6) / 1e9, "launches": e["launches"]}
+                print(f"{name:22s} {fam:34s} {us:9.2f} us {nbytes / 1e6:9.2f} MB "
+                      f"{nbytes / (us * 1e-6) / 1e9:8.1f} GB/s", flush=True)
             for t in outs:
                 t.Dispose()
             compiled.Dispose()
