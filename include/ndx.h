@@ -336,6 +336,14 @@ NDX_API ndx_status ndx_model_run_into_async(ndx_model* model, ndx_tensor* const*
 NDX_API ndx_status ndx_model_run_into_static_async(ndx_model* model, ndx_tensor* const* inputs,
                                                    int32_t n_inputs, ndx_tensor* const* outputs,
                                                    int32_t n_outputs);
+/* GraphChain.Run (Graph/GraphChain.cs:218-282) dispatches one link after
+ * another, each ended by a fence wait (Dml/DmlDevice.cs:908-957). With
+ * replay enabled, ndx_model_run_into_async records the whole run (both
+ * streams) as one HIP graph on its first call and replays it with a single
+ * graph launch on later calls that bind the same input and output tensors
+ * (other tensors record it again). Profiled runs are never replayed. Off by
+ * default; disabling frees the recorded graph. */
+NDX_API ndx_status ndx_model_set_graph_replay(ndx_model* model, int32_t enabled);
 /* Kernel timing with no reference counterpart: while enabled, every kernel a
  * run launches is bracketed by HIP events on the device stream. */
 NDX_API ndx_status ndx_model_set_profiling(ndx_model* model, int32_t enabled);

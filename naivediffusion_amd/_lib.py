@@ -112,6 +112,7 @@ SIGNATURES = [
     ("ndx_model_run", i32, [vp, P(vp), i32, P(vp), i32]),
     ("ndx_model_run_into_async", i32, [vp, P(vp), i32, P(vp), i32]),
     ("ndx_model_run_into_static_async", i32, [vp, P(vp), i32, P(vp), i32]),
+    ("ndx_model_set_graph_replay", i32, [vp, i32]),
     ("ndx_model_set_profiling", i32, [vp, i32]),
     ("ndx_model_set_profile_filter", i32, [vp, ctypes.c_char_p]),
     ("ndx_model_profile_entry", i32, [vp, i32, ctypes.c_char_p, i32, P(i64), P(f64), P(f64), P(f64)]),

@@ -207,6 +207,12 @@ struct ndx_model {
   std::vector<int> signal;
   std::vector<hipEvent_t> lane_events;  // [signals..., start join, end join]
   std::map<std::string, ProfEntry> prof;
+  // Graph replay (ndx_model_set_graph_replay): the run's launches captured
+  // once as a HIP graph, for the pointers in graph_key (inputs, outputs,
+  // arena); replayed while a run binds the same ones.
+  bool replay = false;
+  hipGraphExec_t graph_exec = nullptr;
+  std::vector<void*> graph_key;
 };
 
 namespace {
@@ -2135,6 +2141,42 @@ void harvest_filtered(ndx_model* m) {
   m->prof_pending.clear();
 }
 
+// Launches the run as one HIP graph: captured from run_nodes when the
+// bound pointers differ from the captured graph's (the first run, or other
+// tensors), then replayed with one hipGraphLaunch on the device stream. The
+// second lane joins the capture through the run's own fork and join events.
+void run_replay(ndx_model* m, Runner& r, int n_inputs) {
+  std::vector<void*> key;
+  for (int i = 0; i < n_inputs; i++) key.push_back(r.in[i]->ptr);
+  key.insert(key.end(), r.out_ptr.begin(), r.out_ptr.end());
+  key.push_back(r.arena);
+  hipStream_t s = m->dev->stream;
+  if (!m->graph_exec || key != m->graph_key) {
+    if (m->graph_exec) {
+      hip_check(hipStreamSynchronize(s), "graph replay");
+      (void)hipGraphExecDestroy(m->graph_exec);
+      m->graph_exec = nullptr;
+    }
+    hip_check(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    hipGraph_t graph = nullptr;
+    try {
+      run_nodes(m, r, false);
+    } catch (...) {
+      (void)hipStreamEndCapture(s, &graph);
+      if (graph) (void)hipGraphDestroy(graph);
+      (void)hipGetLastError();
+      throw;
+    }
+    hip_check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+    const hipError_t err = hipGraphInstantiate(&m->graph_exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (err != hipSuccess) m->graph_exec = nullptr;
+    hip_check(err, "hipGraphInstantiate");
+    m->graph_key = key;
+  }
+  hip_check(hipGraphLaunch(m->graph_exec, s), "hipGraphLaunch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -2206,7 +2248,10 @@ NDX_API ndx_status ndx_model_run_into_async(ndx_model* m, ndx_tensor* const* inp
     Runner r{m, inputs, {}};
     bind_outputs(m, r, outputs, n_outputs);
     r.arena = model_arena(m);
-    run_nodes(m, r);
+    if (m->replay && !m->profiling)
+      run_replay(m, r, n_inputs);
+    else
+      run_nodes(m, r);
   } catch (const ndx::Error& e) {
     if (e.status == NDX_DEVICE_LOST) m->dev->lost = true;
     set_last_error(e.message);
@@ -2245,6 +2290,19 @@ NDX_API ndx_status ndx_model_run_into_static_async(ndx_model* m, ndx_tensor* con
     return e.status;
   }
   return NDX_OK;
+}
+
+NDX_API ndx_status ndx_model_set_graph_replay(ndx_model* m, int32_t enabled) {
+  NDX_TRY
+  NEED(m);
+  m->replay = enabled != 0;
+  if (!m->replay && m->graph_exec) {
+    hip_check(hipStreamSynchronize(m->dev->stream), "graph replay");
+    (void)hipGraphExecDestroy(m->graph_exec);
+    m->graph_exec = nullptr;
+    m->graph_key.clear();
+  }
+  NDX_CATCH
 }
 
 NDX_API ndx_status ndx_model_set_profiling(ndx_model* m, int32_t enabled) {
@@ -2291,6 +2349,7 @@ NDX_API ndx_status ndx_model_release(ndx_model* m) {
     m->dev->release(m->arena, m->arena_alloc);
   }
   if (m->two_lanes && m->dev->aux) (void)hipStreamSynchronize(m->dev->aux);
+  if (m->graph_exec) (void)hipGraphExecDestroy(m->graph_exec);
   for (auto e : m->events) (void)hipEventDestroy(e);
   for (auto e : m->fevents) (void)hipEventDestroy(e);
   for (auto e : m->lane_events) (void)hipEventDestroy(e);

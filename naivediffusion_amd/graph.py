@@ -391,6 +391,11 @@ class CompiledModel:
             o.Dispose()
         return host
 
+    def SetGraphReplay(self, enabled: bool) -> None:
+        """Record DispatchInto's launches as one HIP graph and replay it while
+        the same input and output tensors are bound (ndx_model_set_graph_replay)."""
+        call("ndx_model_set_graph_replay", self.handle, int(enabled))
+
     def SetProfiling(self, enabled: bool, family: Optional[str] = None) -> None:
         """Per-kernel timing. family: bracket only that kernel family's
         launches, with no wait per run (for a timed region)."""
