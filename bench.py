@@ -11,7 +11,7 @@ block of the same step and scaled to 60 blocks). The per-family breakdown
 comes from one untimed step with every kernel bracketed.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--compute bf16|f32|f16] [--no-cpu-baseline]
-    python bench.py --workload anima|sdxl   # the Anima DiT / SDXL UNet steps (their own lines)
+    python bench.py --workload anima|sdxl|qwen   # the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps
     python bench.py --calibrate-copy    # a plain 1 GiB device copy, for scaling HBM counters
 
 The roofline's `traffic` (HBM bytes per launch of the dominant kernel) is
@@ -283,6 +283,63 @@ def setup_anima(args, dev, seed, DT):
     )
 
 
+def setup_qwen(args, dev, seed, DT):
+    from naivediffusion_amd import qwen, rng
+    from naivediffusion_amd.tensors import HostTensor
+
+    cfg = qwen.QwenImageConfig(blocks=args.blocks or 32)
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    store = compute if compute != DT.Float32 else DT.Float16
+    lat, n_txt, real = 64, 256, 200
+    n_img = lat * lat
+    n = n_img + n_txt
+    weights = qwen.device_weights(dev, cfg, seed, store)
+    model = qwen.build_step_model(dev, cfg, weights, lat, lat, n_txt, compute, bool(args.int8))
+    cond = qwen.conditioning(np.zeros((real, 1), np.float32), n_txt, lat, lat)
+    times = np.stack([qwen.time_embedding(0.5, cfg.time_dim), qwen.time_embedding(0.0, cfg.time_dim)])
+    inputs = [
+        dev.Normal(DT.Float32, [1, cfg.latent_channels, lat, lat], rng.tensor_seed(seed, "latent")),
+        dev.Upload(HostTensor.FromFloats(times.reshape(1, 1, 2, -1))),
+        dev.Normal(DT.Float32, [1, 1, n_txt, cfg.context_width], rng.tensor_seed(seed, "context")),
+        dev.Upload(HostTensor.FromInt32(cond["text_mask"], 1, 1, n_txt, n_txt)),
+        dev.Upload(HostTensor.FromInt32(cond["key_length"], 1, 1, 1, 1)),
+        dev.Upload(HostTensor.FromFloats(cond["cos"].reshape(1, n, 1, 64))),
+        dev.Upload(HostTensor.FromFloats(cond["sin"].reshape(1, n, 1, 64))),
+    ]
+    out = [dev.Empty(DT.Float32, [1, cfg.latent_channels, lat, lat])]
+
+    def cpu():
+        import oracle
+        names = list(qwen.block_weight_shapes(cfg, 0)) + [
+            "time_text_embed.timestep_embedder.linear_1.weight", "time_text_embed.timestep_embedder.linear_2.weight",
+            "modulation.1.weight"]
+        dw = qwen.device_weights(dev, cfg, seed, DT.BFloat16, names)
+        w = {k: t.Download().ToFloats().reshape(t.Shape) for k, t in dw.items()}
+        for t in dw.values():
+            t.Dispose()
+        x = dev.Normal(DT.Float32, [n, cfg.width], rng.tensor_seed(seed, "cpu.x")).Download().ToFloats().reshape(n, -1)
+        _, mod = oracle.qwen_modulation(0.5, w, cfg.time_dim, cfg.width)
+        threads = len(os.sched_getaffinity(0))
+        t0 = time.perf_counter()
+        oracle.qwen_block(x, mod, w, 0, cfg.heads, n_img, cond["cos"], cond["sin"], int(cond["key_length"][0]),
+                          cond["text_mask"])
+        dt = time.perf_counter() - t0
+        return {"value": dt * cfg.blocks, "unit": "s/step", "cores": threads, "kind": "port",
+                "sample": (f"one Qwen-Image 2.1 block ({n_img} image + {n_txt} text tokens, width {cfg.width}, fp32) "
+                           f"on the oracle in {dt:.2f} s, x{cfg.blocks} blocks (extrapolated)")}
+
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="Qwen-Image 2.1 DiT s/step @1024x1024, 1 MI355X; % MFMA peak",
+        config={"workload": (f"Qwen-Image 2.1 single-stream DiT denoiser step, {cfg.blocks} blocks, 1024x1024 "
+                             f"(latent 64x{lat}x{lat}, patch 1: {n_img} image + {n_txt} text rows, {real} real), "
+                             f"hidden 4096, 32x128 heads, SwiGLU 12288, batch 1, {args.compute} compute"),
+                "blocks": cfg.blocks, "image_tokens": n_img, "text_rows": n_txt},
+        data="synthetic (seeded N(0,1) latent and context, N(0,0.02) weights made on the GPU)",
+        cpu=cpu,
+    )
+
+
 def setup_sdxl(args, dev, seed, DT):
     from naivediffusion_amd import rng, sdxl
     from naivediffusion_amd.tensors import HostTensor
@@ -316,8 +373,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl"], default="mmdit",
-                    help="mmdit (the headline), or the Anima DiT / SDXL UNet steps")
+    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl", "qwen"], default="mmdit",
+                    help="mmdit (the headline), or the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps")
     ap.add_argument("--compute", choices=["bf16", "f32", "f16"], default=None,
                     help="compute type (default bf16; fp16 for sdxl)")
     ap.add_argument("--int8", nargs="?", const="block32", default=None, choices=["block32", "channel"],
@@ -352,7 +409,8 @@ def main():
     dev = nd.Device()
     log(f"device {dev.AdapterName}")
     t0 = time.perf_counter()
-    setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl}[args.workload](args, dev, seed, DT)
+    setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl, "qwen": setup_qwen}[args.workload](
+        args, dev, seed, DT)
     compiled = setup["model"].Compiled
     log(f"graph built and compiled in {time.perf_counter() - t0:.1f} s: {compiled.KernelCount} kernels/step, "
         f"{compiled.PersistentSize / 1e9:.1f} GB weights, {compiled.TemporarySize / 1e9:.2f} GB scratch")

@@ -223,9 +223,18 @@ enum {
     NDX_EPI_GATED_RESIDUAL = 4, /* out = aux1 + aux0 * Cast(product, aux1.dtype):
                                    the gated residual of QwenImageDit.cs:421,425 and
                                    Models/Anima/AnimaDit.cs:344,349,355; aux0 is a
-                                   [.., 1, N] gate broadcast over rows, aux1 the
-                                   residual [.., M, N]; out takes aux1's dtype */
-    NDX_EPI_RESIDUAL = 5        /* out = aux1 + Cast(product, aux1.dtype) */
+                                   [.., 1, N] gate broadcast over rows or a
+                                   [.., M, N] gate per row (a join of two row
+                                   broadcasts, QwenImageDit.cs:307-315, is read
+                                   in place), aux1 the residual [.., M, N]; out
+                                   takes aux1's dtype */
+    NDX_EPI_RESIDUAL = 5,       /* out = aux1 + Cast(product, aux1.dtype) */
+    NDX_EPI_SWIGLU = 6          /* SwiGLU, Models/QwenImage/QwenImageDit.cs:390-406:
+                                   W's rows interleave the gate and up projections
+                                   (row 2j gate j, row 2j+1 up j); out[j] =
+                                   SiLU(gate_j) * up_j with gate, up and the SiLU
+                                   rounded to x's dtype as the reference's separate
+                                   operators are; out has N/2 columns */
 };
 /* Layers.Linear, Graph/Layers.cs:131-160 (DmlOps.Gemm with transB,
  * Dml/DmlOps.cs:231-262): y = x[.., M, K] * W[N, K]^T (+ bias[N]) then the
@@ -263,7 +272,9 @@ NDX_API ndx_status ndx_op_layer_norm(ndx_graph* graph, ndx_value x, ndx_value we
                                      ndx_value bias, float eps, ndx_value* out);
 /* Transformer.Modulate, Graph/Transformer.cs:72-80:
  * Cast(LayerNorm(x) * (1 + scale) + shift, out_dtype); shift may be NONE;
- * scale and shift are [.., 1, D] rows broadcast over tokens. */
+ * scale and shift are [.., 1, D] rows broadcast over tokens, or [.., T, D]
+ * per token (a join of two row broadcasts, the image and text rows of
+ * QwenImageDit.cs:307-315, is read in place without being materialised). */
 NDX_API ndx_status ndx_op_modulate(ndx_graph* graph, ndx_value x, ndx_value shift,
                                    ndx_value scale, float eps, int32_t out_dtype,
                                    ndx_value* out);

@@ -67,6 +67,10 @@ struct GNode {
   float f0 = 0.f, f1 = 0.f;
   // attention segments (compile-time rewrite): per q/k/v up to two values
   int seg[3][2] = {{-1, -1}, {-1, -1}, {-1, -1}};
+  // Two-row operands (compile-time rewrite of a join of two row broadcasts):
+  // per operand slot, the first row from rows_split on is rows_off elements
+  // past the one the operand's view starts at (0: not split).
+  int64_t rows_split[5] = {0, 0, 0, 0, 0}, rows_off[5] = {0, 0, 0, 0, 0};
   // scratch in the arena, live only while this node runs
   int64_t scratch_bytes = 0, scratch_off = -1;
   // the stream (0 the device's, 1 the second) the node runs on
@@ -718,7 +722,8 @@ NDX_API ndx_status ndx_op_linear(ndx_graph* g, ndx_value x, ndx_value w, ndx_val
     require_float(vb, "the bias");
     if (numel4(vb.v) != N) fail(NDX_INVALID_ARG, "the bias must have one value per output feature");
   }
-  if (epilogue < 0 || epilogue > 5) fail(NDX_INVALID_ARG, "unknown epilogue");
+  if (epilogue < 0 || epilogue > NDX_EPI_SWIGLU) fail(NDX_INVALID_ARG, "unknown epilogue");
+  if (epilogue == NDX_EPI_SWIGLU && N % 2) fail(NDX_INVALID_ARG, "a SwiGLU needs interleaved gate and up rows (an even count)");
   int out_dtype = vx.dtype;
   if (epilogue == NDX_EPI_GATED_RESIDUAL || epilogue == NDX_EPI_RESIDUAL) {
     if (aux1 == NDX_NONE) fail(NDX_INVALID_ARG, "a residual epilogue needs the residual");
@@ -731,7 +736,8 @@ NDX_API ndx_status ndx_op_linear(ndx_graph* g, ndx_value x, ndx_value w, ndx_val
       if (aux0 == NDX_NONE) fail(NDX_INVALID_ARG, "a gated residual needs the gate");
       GValue& gt = g->val(aux0);
       require_float(gt, "the gate");
-      if (gt.v.size[3] != N || gt.v.size[2] != 1) fail(NDX_INVALID_ARG, "the gate must be a [.., 1, N] row");
+      if (gt.v.size[3] != N || (gt.v.size[2] != 1 && gt.v.size[2] != M))
+        fail(NDX_INVALID_ARG, "the gate must be a [.., 1, N] row or [.., M, N]");
       if ((gt.v.size[0] != 1 && gt.v.size[0] != vx.v.size[0]) || (gt.v.size[1] != 1 && gt.v.size[1] != vx.v.size[1]))
         fail(NDX_INVALID_ARG, "the gate's batch does not match the input's");
     }
@@ -740,7 +746,7 @@ NDX_API ndx_status ndx_op_linear(ndx_graph* g, ndx_value x, ndx_value w, ndx_val
   n.op = OP_LINEAR;
   n.in = {x, w, bias, aux0, aux1};
   n.i0 = epilogue;
-  int64_t size[4] = {vx.v.size[0], vx.v.size[1], M, N};
+  int64_t size[4] = {vx.v.size[0], vx.v.size[1], M, epilogue == NDX_EPI_SWIGLU ? N / 2 : N};
   *out = g->emit(n, out_dtype, size, vx.rank);
   NDX_CATCH
 }
@@ -869,7 +875,8 @@ static int row_norm(ndx_graph* g, int mode, int x, int w, int b, float eps, int 
     GValue& p = g->val(id);
     require_float(p, "a norm parameter");
     if (p.v.size[3] != D) fail(NDX_INVALID_ARG, "a norm parameter must span the normalised axis");
-    if (p.v.size[2] != 1) fail(NDX_INVALID_ARG, "a norm parameter is one row (per batch)");
+    if (p.v.size[2] != 1 && p.v.size[2] != vx.v.size[2])
+      fail(NDX_INVALID_ARG, "a norm parameter is one row (per batch) or one per row");
   }
   GNode n;
   n.op = OP_ROWNORM;
@@ -1320,6 +1327,54 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     }
   }
 
+  // Rewrite: a join along the tokens of two broadcasts of single rows of
+  // one value, read as a Modulate's scale or shift or a gated residual's
+  // gate (the image and text rows of Models/QwenImage/QwenImageDit.cs:
+  // 307-315), is never materialised: the operand becomes the first
+  // broadcast, and the node reads the second row from the split on.
+  auto two_rows = [&](int id, int64_t& split, int64_t& off) -> int {
+    const GValue& v = c.values[id];
+    if (v.kind != VK_NODE || v.base != id || v.producer < 0 || v.v.size[2] <= 1) return -1;
+    const GNode& p = src[v.producer];
+    if (p.op != OP_JOIN || p.in.size() != 2 || p.i0 != 2) return -1;
+    const GValue& a = c.values[p.in[0]];
+    const GValue& b = c.values[p.in[1]];
+    if (a.base != b.base || a.dtype != b.dtype || c.values[a.base].quant) return -1;
+    for (const GValue* e : {&a, &b})
+      if ((e->v.size[2] > 1 && e->v.stride[2] != 0) || (e->v.size[3] > 1 && e->v.stride[3] != 1) ||
+          e->v.size[0] != v.v.size[0] ||
+          e->v.size[1] != v.v.size[1])
+        return -1;
+    if (a.v.stride[0] != b.v.stride[0] || a.v.stride[1] != b.v.stride[1]) return -1;
+    split = a.v.size[2];
+    off = b.offset - a.offset;
+    return p.in[0];
+  };
+  for (auto& n : src) {
+    if (n.op == OP_LINEAR && n.i0 == EPI_GATED_RESIDUAL && n.in[3] >= 0) {
+      int64_t split, off;
+      const int first = two_rows(n.in[3], split, off);
+      if (first >= 0) {
+        n.in[3] = first;
+        n.rows_split[3] = split;
+        n.rows_off[3] = off;
+      }
+    } else if (n.op == OP_ROWNORM) {
+      int64_t split[3] = {0, 0, 0}, off[3] = {0, 0, 0};
+      int first[3] = {-1, -1, -1};
+      for (int j = 1; j < 3; j++)
+        if (n.in[j] >= 0) first[j] = two_rows(n.in[j], split[j], off[j]);
+      // The kernel takes one split for the weight and the bias.
+      if (first[1] >= 0 && first[2] >= 0 && split[1] != split[2]) first[2] = -1;
+      for (int j = 1; j < 3; j++)
+        if (first[j] >= 0) {
+          n.in[j] = first[j];
+          n.rows_split[j] = split[j];
+          n.rows_off[j] = off[j];
+        }
+    }
+  }
+
   // Rewrite: x * Gelu(y), the GELU's output read by this product only (the
   // GEGLU of SDXL's feed-forward, Models/Sdxl/UNetLayers.cs), becomes one
   // elementwise pass; the GELU node is then unreachable and never runs.
@@ -1382,6 +1437,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         if (n.in[3] >= 0) {
           const GValue& gt = c.values[n.in[3]];
           if (gt.v.size[3] > 1 && gt.v.stride[3] != 1) n.in[3] = c.pack(n.in[3], sched);
+          else if (gt.v.size[2] > 1 && !n.rows_split[3]) ensure_rows(n.in[3]);
         }
         {
           const GValue& w = c.values[n.in[1]];
@@ -1409,9 +1465,12 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         break;
       case OP_ROWNORM:
         ensure_rows(n.in[0]);
-        for (int j = 1; j < 3; j++)
-          if (n.in[j] >= 0 && c.values[n.in[j]].v.size[3] > 1 && c.values[n.in[j]].v.stride[3] != 1)
-            n.in[j] = c.pack(n.in[j], sched);
+        for (int j = 1; j < 3; j++) {
+          if (n.in[j] < 0) continue;
+          const GValue& pv = c.values[n.in[j]];
+          if (pv.v.size[3] > 1 && pv.v.stride[3] != 1) n.in[j] = c.pack(n.in[j], sched);
+          else if (pv.v.size[2] > 1 && !n.rows_split[j]) ensure_rows(n.in[j]);
+        }
         break;
       case OP_GROUPNORM: {
         for (auto& id : n.in)
@@ -1657,9 +1716,13 @@ struct Runner {
     a.batch_w = 0;
     a.tile_hint = second_stream_tile(n, a.M);
     a.c = ptr(n.out);
-    a.ldc = a.N;
-    a.batch_c = int64_t(a.M) * a.N;
+    // A SwiGLU writes one column per interleaved (gate, up) pair: N / 2.
+    a.ldc = n.i0 == EPI_SWIGLU ? a.N / 2 : a.N;
+    a.batch_c = int64_t(a.M) * a.ldc;
     a.c_dtype = o.dtype;
+    // Every row the product writes must lie in its output's buffer.
+    if (o.offset + int64_t(a.batch) * a.batch_c > m->values[o.base].buffer_elems)
+      fail(NDX_INVALID_STATE, "a linear's output rows overrun its buffer");
     if (n.in[2] >= 0) {
       a.bias = ptr(n.in[2]);
       a.bias_dtype = val(n.in[2]).dtype;
@@ -1670,6 +1733,9 @@ struct Runner {
       a.gate = ptr(n.in[3]);
       a.gate_dtype = gt.dtype;
       a.batch_gate = (gt.v.size[0] > 1) ? gt.v.stride[0] : (gt.v.size[1] > 1 ? gt.v.stride[1] : 0);
+      a.ldg = gt.v.size[2] > 1 ? gt.v.stride[2] : 0;
+      a.gate_split = n.rows_split[3];
+      a.gate_split_off = n.rows_off[3];
     }
     if (n.in[4] >= 0) {
       const GValue& r = val(n.in[4]);
@@ -1860,16 +1926,21 @@ struct Runner {
         // A row's source offset: (row / rows_per_batch) * bs + (row % rows_per_batch) * ld.
         a.mode = n.i0;
         a.eps = n.f0;
-        auto param = [&](int id, const void*& p, int64_t& batch, int& dt) {
+        auto param = [&](int id, const void*& p, int64_t& batch, int64_t& ld, int& dt) {
           if (id < 0) return;
           const GValue& pv = val(id);
           p = ptr(id);
           dt = pv.dtype;
-          // Per-batch rows (modulation) when the parameter has a batch > 1.
+          // Per-batch rows (modulation) when the parameter has a batch > 1,
+          // a row per token when it has tokens.
           batch = pv.v.size[0] > 1 ? pv.v.stride[0] : (pv.v.size[1] > 1 ? pv.v.stride[1] : 0);
+          ld = pv.v.size[2] > 1 ? pv.v.stride[2] : 0;
         };
-        param(n.in[1], a.weight, a.batch_w, a.w_dtype);
-        param(n.in[2], a.bias, a.batch_b, a.b_dtype);
+        param(n.in[1], a.weight, a.batch_w, a.ldw, a.w_dtype);
+        param(n.in[2], a.bias, a.batch_b, a.ldb, a.b_dtype);
+        a.split = std::max(n.rows_split[1], n.rows_split[2]);
+        a.split_w_off = n.rows_off[1];
+        a.split_b_off = n.rows_off[2];
         a.batch_x = bs;
         launch_row_norm(a, s);
         break;

@@ -69,6 +69,12 @@ __device__ __forceinline__ float scale_at(const void* s, int sdt, int64_t i) {
   return sdt == NDX_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
 }
 
+// Element offset of the gate of (b, row, col = 0): one row for all rows
+// (ldg 0), a row per row, or two rows split at gate_split.
+__device__ __forceinline__ int64_t gate_off(const GemmArgs& a, int64_t b, int row) {
+  return b * a.batch_gate + int64_t(row) * a.ldg + (row >= a.gate_split ? a.gate_split_off : 0);
+}
+
 // The epilogue of one output element (row, col) of batch b.
 __device__ __forceinline__ void epilogue_one(const GemmArgs& a, int64_t b, int row, int col, float v, float bias,
                                              float gate) {
@@ -99,6 +105,18 @@ __device__ __forceinline__ float4 load4_vec(const void* p, int dt, int64_t off) 
   }
   const _Float16* h = (const _Float16*)&u;
   return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+__device__ __forceinline__ bool aligned16(const void* p, int64_t elems_a, int64_t elems_b, int es) {
+  return (uintptr_t)p % 16 == 0 && (elems_a * es) % 16 == 0 && (elems_b * es) % 16 == 0;
+}
+
+// Up to four per-column values p[off .. off + n) (zeros past n).
+__device__ __forceinline__ float4 load_cols(const void* p, int dt, int64_t off, int n, bool vec) {
+  if (n >= 4 && vec) return load4_vec(p, dt, off);
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < n && e < 4; e++) v[e] = load_f(p, dt, off + e);
+  return make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // Stores four consecutive outputs in one 16-byte (fp32) or 8-byte (16-bit)
@@ -136,11 +154,29 @@ __device__ __forceinline__ void epilogue_fast(const GemmArgs& a, int64_t b, int 
 // the residual are read here; GELU-tanh, GELU or SiLU, or the (gated)
 // residual; vector stores where all four are there and vec allows.
 __device__ __forceinline__ void epilogue_any(const GemmArgs& a, int64_t b, int row, int col, int n, float4 acc,
-                                             float4 bias, float4 gate, bool vec) {
+                                             float4 bias, float4 gate, bool vec, bool gate_rows = false) {
   if (row >= a.M || n <= 0) return;
   const float rb = a.row_bias ? load_f(a.row_bias, a.row_bias_dtype, row) : 0.f;
   float v[4] = {acc.x + bias.x + rb, acc.y + bias.y + rb, acc.z + bias.z + rb, acc.w + bias.w + rb};
   const int ep = a.epilogue;
+  if (ep == EPI_SWIGLU) {
+    // Columns col .. col + 3 (col a multiple of 4) are two (gate, up) pairs
+    // of the interleaved projection: outputs col / 2 and col / 2 + 1. The
+    // gate, the up projection and the SiLU are each rounded to the product's
+    // type, as the reference's separate operators leave them.
+    float o[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const float g = round_to(v[2 * p], a.a_dtype), u = round_to(v[2 * p + 1], a.a_dtype);
+      o[p] = round_to(silu_f(g), a.a_dtype) * u;
+    }
+    const int64_t co = b * a.batch_c + int64_t(row) * a.ldc + col / 2;
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+      if (2 * p + 1 < n) store_f(a.c, a.c_dtype, co + p, o[p]);
+    return;
+  }
+  if (gate_rows && ep == EPI_GATED_RESIDUAL) gate = load_cols(a.gate, a.gate_dtype, gate_off(a, b, row) + col, n, false);
   if (ep == EPI_GELU_TANH) {
 #pragma unroll
     for (int e = 0; e < 4; e++) v[e] = gelu_tanh_f(v[e]);
@@ -167,24 +203,12 @@ __device__ __forceinline__ void epilogue_any(const GemmArgs& a, int64_t b, int r
     if (e < n) store_f(a.c, a.c_dtype, co + e, v[e]);
 }
 
-__device__ __forceinline__ bool aligned16(const void* p, int64_t elems_a, int64_t elems_b, int es) {
-  return (uintptr_t)p % 16 == 0 && (elems_a * es) % 16 == 0 && (elems_b * es) % 16 == 0;
-}
-
-// Up to four per-column values p[off .. off + n) (zeros past n).
-__device__ __forceinline__ float4 load_cols(const void* p, int dt, int64_t off, int n, bool vec) {
-  if (n >= 4 && vec) return load4_vec(p, dt, off);
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int e = 0; e < n && e < 4; e++) v[e] = load_f(p, dt, off + e);
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-
 // What every slice of a wave's epilogue shares: the lane's columns, the
 // bias and gate of those columns, and which epilogue path runs.
 struct EpiLane {
   int col, n, c4, rl0;
-  float4 bias, gate;
-  bool fast, out_vec;
+  float4 bias, gate, gate2;  // gate2: the gate of rows at or past gate_split
+  bool fast, out_vec, gate_rows;
 };
 
 // One 32-row slice (accumulator row block i of the wave) through LDS, so
@@ -227,14 +251,16 @@ __device__ __forceinline__ void epilogue_slice(const GemmArgs& a, int64_t bidx, 
     for (int t = 0; t < IT; t++) {
       const int rl = L.rl0 + t * RSTEP;
       const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
-      epilogue_fast(a, bidx, row0 + rl, L.col, v, L.bias, rb[t], L.gate, res[t]);
+      epilogue_fast(a, bidx, row0 + rl, L.col, v, L.bias, rb[t], row0 + rl >= a.gate_split ? L.gate2 : L.gate,
+                    res[t]);
     }
   } else {
 #pragma unroll 1
     for (int t = 0; t < IT; t++) {
       const int rl = L.rl0 + t * RSTEP;
       const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
-      epilogue_any(a, bidx, row0 + rl, L.col, L.n, v, L.bias, L.gate, L.out_vec);
+      epilogue_any(a, bidx, row0 + rl, L.col, L.n, v, L.bias, row0 + rl >= a.gate_split ? L.gate2 : L.gate,
+                   L.out_vec, L.gate_rows);
     }
   }
   __syncthreads();
@@ -269,17 +295,25 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx,
   L.n = min(4, a.N - L.col);
   const int ep = a.epilogue;
   const bool residual = ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL;
-  const bool act = ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU;
+  const bool act = ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU || ep == EPI_SWIGLU;
   L.out_vec = aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype));
   const bool res_vec = residual && aligned16(a.resid, a.ldr, a.batch_r, dtype_size(a.r_dtype));
+  // A gate per row is read per row; one or two gate rows once per lane.
+  L.gate_rows = ep == EPI_GATED_RESIDUAL && a.ldg != 0;
   // Uniform over the wave: all of its columns in range, aligned rows.
-  L.fast = !act && col0 + WN <= a.N && L.out_vec && (!residual || res_vec);
+  L.fast = !act && !L.gate_rows && col0 + WN <= a.N && L.out_vec && (!residual || res_vec);
   L.bias = make_float4(0.f, 0.f, 0.f, 0.f);
   L.gate = make_float4(1.f, 1.f, 1.f, 1.f);
+  L.gate2 = L.gate;
   if (L.n > 0 && a.bias) L.bias = load_cols(a.bias, a.bias_dtype, L.col, L.n, (uintptr_t)a.bias % 16 == 0);
-  if (L.n > 0 && ep == EPI_GATED_RESIDUAL)
-    L.gate = load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + L.col, L.n,
-                       aligned16(a.gate, a.batch_gate, 0, dtype_size(a.gate_dtype)));
+  if (L.n > 0 && ep == EPI_GATED_RESIDUAL && !L.gate_rows) {
+    const int gs = dtype_size(a.gate_dtype);
+    L.gate = load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + L.col, L.n, aligned16(a.gate, a.batch_gate, 0, gs));
+    L.gate2 = a.gate_split_off == 0
+                  ? L.gate
+                  : load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + a.gate_split_off + L.col, L.n,
+                              aligned16(a.gate, a.batch_gate, a.gate_split_off, gs));
+  }
   epilogue_slices<0, TM, TN, WN>(a, bidx, L, acc, stage, row0);
 }
 
@@ -1160,7 +1194,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs a) {
       const float v = wave_sum(acc[q][m]);
       if (lane == 0 && m < a.M && n < a.N) {
         const float bias = a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f;
-        const float gate = a.gate ? load_f(a.gate, a.gate_dtype, bidx * a.batch_gate + n) : 0.f;
+        const float gate = a.gate ? load_f(a.gate, a.gate_dtype, gate_off(a, bidx, m) + n) : 0.f;
         epilogue_one(a, bidx, m, n, v, bias, gate);
       }
     }
@@ -1261,7 +1295,7 @@ static int pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch, double* mod
 static GemmKind choose(const GemmArgs& a) {
   const int MR = a.M;
   if (!w_aligned(a)) return K_GENERIC_LINEAR;
-  if (MR <= 4 && int64_t(4) * a.K * 4 <= 65536 && a.K % 8 == 0) return K_GEMV;
+  if (MR <= 4 && int64_t(4) * a.K * 4 <= 65536 && a.K % 8 == 0 && a.epilogue != EPI_SWIGLU) return K_GEMV;
   if (!a_aligned(a) || !spans_fit(a)) return K_GENERIC_LINEAR;
   if (a.w_dtype == NDX_I8 && ((uintptr_t)a.w % 16 || a.ldw % 16)) return K_GENERIC_LINEAR;
   if ((a.a_dtype == NDX_BF16 || a.a_dtype == NDX_F16) && a.K % 16 == 0) {
@@ -1323,7 +1357,36 @@ const char* gemm_family(const GemmArgs& a) {
   }
 }
 
+// The interleaved SwiGLU in the generic kernel: output j of row m from
+// the gate (row 2j of W) and up (row 2j + 1) dot products.
+__device__ __forceinline__ float generic_dot(const GemmArgs& a, int64_t b, int m, int n) {
+  float acc = 0.f;
+  for (int k = 0; k < a.K; k++) {
+    float w = a.w_dtype == NDX_I8
+                  ? float(((const int8_t*)a.w)[int64_t(n) * a.ldw + k]) *
+                        scale_at(a.scales, a.s_dtype, int64_t(n) * a.lds + k / a.qblock)
+                  : load_f(a.w, a.w_dtype, int64_t(n) * a.ldw + k);
+    acc += load_f(a.a, a.a_dtype, b * a.batch_a + int64_t(m) * a.lda + k) * w;
+  }
+  return acc + (a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f);
+}
+
 __global__ void linear_generic_kernel(GemmArgs a) {
+  if (a.epilogue == EPI_SWIGLU) {
+    const int NO = a.N / 2;
+    const int64_t total = int64_t(a.batch) * a.M * NO;
+    for (int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; id < total;
+         id += int64_t(gridDim.x) * blockDim.x) {
+      const int j = (int)(id % NO);
+      const int64_t r = id / NO;
+      const int m = (int)(r % a.M);
+      const int64_t b = r / a.M;
+      const float g = round_to(generic_dot(a, b, m, 2 * j), a.a_dtype);
+      const float u = round_to(generic_dot(a, b, m, 2 * j + 1), a.a_dtype);
+      store_f(a.c, a.c_dtype, b * a.batch_c + int64_t(m) * a.ldc + j, round_to(silu_f(g), a.a_dtype) * u);
+    }
+    return;
+  }
   const int64_t total = int64_t(a.batch) * a.M * a.N;
   for (int64_t id = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; id < total;
        id += int64_t(gridDim.x) * blockDim.x) {
@@ -1340,7 +1403,7 @@ __global__ void linear_generic_kernel(GemmArgs a) {
       acc += load_f(a.a, a.a_dtype, b * a.batch_a + int64_t(m) * a.lda + k) * w;
     }
     const float bias = a.bias ? load_f(a.bias, a.bias_dtype, n) : 0.f;
-    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, b * a.batch_gate + n) : 0.f;
+    const float gate = a.gate ? load_f(a.gate, a.gate_dtype, gate_off(a, b, m) + n) : 0.f;
     epilogue_one(a, b, m, n, acc, bias, gate);
   }
 }

@@ -9,6 +9,13 @@
 
 namespace ndx {
 
+// Offsets of row `within` (of batch `batch`) into the weight and bias: one
+// row for all (ld 0), a row per row, or two rows split at `split`.
+__device__ __forceinline__ int64_t param_off(int64_t batch, int64_t within, int64_t bstride, int64_t ld, int64_t split,
+                                             int64_t split_off) {
+  return batch * bstride + within * ld + (within >= split ? split_off : 0);
+}
+
 // One 64-lane wave per row; lane l holds elements l, l + 64, ... so every
 // load and store of the wave is one contiguous run. VPT values per lane stay
 // in registers between the statistics and the output pass.
@@ -49,7 +56,8 @@ __global__ __launch_bounds__(256) void row_norm_kernel(RowNormArgs a) {
     ss = wave_sum(ss);
     rstd = 1.0f / sqrtf(ss / D + a.eps);
   }
-  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  const int64_t woff = param_off(batch, row % a.rows_per_batch, a.batch_w, a.ldw, a.split, a.split_w_off),
+                boff = param_off(batch, row % a.rows_per_batch, a.batch_b, a.ldb, a.split, a.split_b_off);
   const int64_t yoff = row * a.ldy;
 #pragma unroll
   for (int j = 0; j < VPT; j++) {
@@ -111,7 +119,8 @@ __global__ __launch_bounds__(256) void row_norm_wide_kernel(RowNormArgs a) {
     q = red[0][0] + red[0][1] + red[0][2] + red[0][3];
     rstd = 1.0f / sqrtf(q / D + a.eps);
   }
-  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  const int64_t woff = param_off(batch, row % a.rows_per_batch, a.batch_w, a.ldw, a.split, a.split_w_off),
+                boff = param_off(batch, row % a.rows_per_batch, a.batch_b, a.ldb, a.split, a.split_b_off);
   for (int c = t; c < D; c += 256) {
     float n = (load_f(a.x, a.x_dtype, xoff + c) - mean) * rstd;
     float y;
@@ -184,7 +193,8 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(RowNormArgs a) {
     ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
   }
   const float rstd = 1.0f / sqrtf(wave_sum(ss) * (1.0f / D) + a.eps);
-  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  const int64_t woff = param_off(batch, row % a.rows_per_batch, a.batch_w, a.ldw, a.split, a.split_w_off),
+                boff = param_off(batch, row % a.rows_per_batch, a.batch_b, a.ldb, a.split, a.split_b_off);
   const int64_t yoff = row * a.ldy;
 #pragma unroll
   for (int j = 0; j < NC; j++) {
@@ -253,7 +263,8 @@ __global__ __launch_bounds__(256) void row_norm_f32_kernel(RowNormArgs a) {
   const int64_t batch = row / a.rows_per_batch;
   const int64_t xoff = batch * a.batch_x + (row % a.rows_per_batch) * a.ldx;
   constexpr int D = NC * 256;
-  const int64_t woff = batch * a.batch_w, boff = batch * a.batch_b;
+  const int64_t woff = param_off(batch, row % a.rows_per_batch, a.batch_w, a.ldw, a.split, a.split_w_off),
+                boff = param_off(batch, row % a.rows_per_batch, a.batch_b, a.ldb, a.split, a.split_b_off);
   float4 v[NC], w[NC], bb[NC];
 #pragma unroll
   for (int j = 0; j < NC; j++) v[j] = load4_t<NDX_F32>(a.x, xoff + (j * 64 + lane) * 4);
@@ -305,8 +316,8 @@ void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
   int vpt = (a.D + 63) / 64;
   dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
   const bool vec = a.D % 256 == 0 && a.D <= 4096 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) &&
-                   vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, 0, a.batch_w) &&
-                   vec_ok(a.bias, a.b_dtype, 0, a.batch_b);
+                   vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, a.ldw, a.batch_w) && vec_ok(a.weight, a.w_dtype, 0, a.split_w_off) &&
+                   vec_ok(a.bias, a.b_dtype, a.ldb, a.batch_b) && vec_ok(a.bias, a.b_dtype, 0, a.split_b_off);
   const bool f32_terms = a.x_dtype == NDX_F32 && (!a.weight || a.w_dtype == NDX_F32) &&
                          (!a.bias || a.b_dtype == NDX_F32);
   if (vec && f32_terms && (a.D == 2048 || a.D == 3072 || a.D == 4096)) {
@@ -338,8 +349,8 @@ void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
     }
   }
   const bool part = a.D % 4 == 0 && a.D % 256 != 0 && a.D < 2048 && vec_ok(a.x, a.x_dtype, a.ldx, a.batch_x) &&
-                    vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, 0, a.batch_w) &&
-                    vec_ok(a.bias, a.b_dtype, 0, a.batch_b);
+                    vec_ok(a.y, a.y_dtype, a.ldy, 0) && vec_ok(a.weight, a.w_dtype, a.ldw, a.batch_w) && vec_ok(a.weight, a.w_dtype, 0, a.split_w_off) &&
+                    vec_ok(a.bias, a.b_dtype, a.ldb, a.batch_b) && vec_ok(a.bias, a.b_dtype, 0, a.split_b_off);
   if (part) {
     switch ((a.D + 255) / 256) {
       case 1: hipLaunchKernelGGL((row_norm_vec_kernel<1, true>), grid, block, 0, s, a); return;

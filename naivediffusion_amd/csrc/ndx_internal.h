@@ -55,6 +55,7 @@ enum Epilogue {
   EPI_SILU = NDX_EPI_SILU,
   EPI_GATED_RESIDUAL = NDX_EPI_GATED_RESIDUAL,
   EPI_RESIDUAL = NDX_EPI_RESIDUAL,
+  EPI_SWIGLU = NDX_EPI_SWIGLU,
 };
 
 // One linear layer's product: C[b] = epi(A[b] (M x K, rows lda apart) *
@@ -66,7 +67,11 @@ struct GemmArgs {
   const void* scales; int64_t lds; int qblock; int s_dtype;  // int8 weights only
   void* c; int64_t ldc; int64_t batch_c; int c_dtype;
   const void* bias; int bias_dtype;
+  // The gate of (b, row, col): b * batch_gate + row * ldg + col, plus
+  // gate_split_off for rows at or past gate_split (ldg 0: one row for all;
+  // the split: two such rows, the reference's join of two row broadcasts).
   const void* gate; int64_t batch_gate; int gate_dtype;
+  int64_t ldg, gate_split, gate_split_off;
   const void* resid; int64_t ldr; int64_t batch_r; int r_dtype;
   int M, N, K, batch;
   int epilogue;
@@ -133,6 +138,10 @@ struct RowNormArgs {
   int64_t rows_per_batch;            // batch index = row / rows_per_batch
   const void* weight; int64_t batch_w; int w_dtype;   // LN weight / (1+scale) / RMS weight
   const void* bias; int64_t batch_b; int b_dtype;     // LN bias / shift
+  // Row r (within its batch) reads weight/bias at batch * batch_w + r * ldw
+  // (ldw 0: one row for all), plus split_w_off / split_b_off when r >= split
+  // (two rows: the reference's join of two row broadcasts).
+  int64_t ldw, ldb, split, split_w_off, split_b_off;
   float eps;
   int mode;   // 0 layernorm(+affine), 1 modulate, 2 rmsnorm
 };

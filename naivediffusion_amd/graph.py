@@ -24,7 +24,7 @@ NONE = -1
 # ndx.h enums
 UNARY_IDENTITY, UNARY_SIGMOID, UNARY_SILU, UNARY_GELU, UNARY_TANH, UNARY_GELU_TANH = range(6)
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
-EPI_NONE, EPI_GELU_TANH, EPI_GELU, EPI_SILU, EPI_GATED_RESIDUAL, EPI_RESIDUAL = range(6)
+EPI_NONE, EPI_GELU_TANH, EPI_GELU, EPI_SILU, EPI_GATED_RESIDUAL, EPI_RESIDUAL, EPI_SWIGLU = range(7)
 PATCH_CHANNEL_FIRST, PATCH_CHANNEL_LAST = 0, 1  # feature order (c, dy, dx) or (dy, dx, c)
 
 

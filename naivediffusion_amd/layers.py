@@ -16,7 +16,8 @@ from typing import Optional, Union
 import numpy as np
 
 from ._lib import ArgumentError
-from .graph import (EPI_GATED_RESIDUAL, EPI_GELU, EPI_GELU_TANH, EPI_NONE, EPI_RESIDUAL, EPI_SILU, Expression,
+from .graph import (EPI_GATED_RESIDUAL, EPI_GELU, EPI_GELU_TANH, EPI_NONE, EPI_RESIDUAL, EPI_SILU, EPI_SWIGLU,
+                    Expression,
                     MaskType, ModelBuilder, Ops)
 from .tensors import HostDataType, HostTensor
 
@@ -106,9 +107,12 @@ class Layers:
         weights, the product at x's precision (a narrower weight is widened in
         the kernel), the weight shared across the batch.
 
-        Fused tails: activation 'gelu_tanh' | 'gelu' | 'silu'; with residual,
-        residual + Cast(y) (or residual + gate * Cast(y) with gate, the gated
-        residual of QwenImageDit.cs:421,425), at the residual's precision."""
+        Fused tails: activation 'gelu_tanh' | 'gelu' | 'silu', or 'swiglu'
+        (SiLU(gate) * up over a weight whose rows interleave the gate and up
+        projections, QwenImageDit.cs:390-406; half the columns out); with
+        residual, residual + Cast(y) (or residual + gate * Cast(y) with gate,
+        the gated residual of QwenImageDit.cs:421,425), at the residual's
+        precision."""
         if isinstance(weight, HostTensor):
             out_features, in_features = weight.Shape[0], weight.Shape[1]
             w = model.Weight(weight, [1, 1, out_features, in_features], out_features)
@@ -124,7 +128,7 @@ class Layers:
                 raise ArgumentError("an activation and a residual do not fuse together")
             epi = EPI_GATED_RESIDUAL if gate is not None else EPI_RESIDUAL
         elif activation is not None:
-            epi = {"gelu_tanh": EPI_GELU_TANH, "gelu": EPI_GELU, "silu": EPI_SILU}[activation]
+            epi = {"gelu_tanh": EPI_GELU_TANH, "gelu": EPI_GELU, "silu": EPI_SILU, "swiglu": EPI_SWIGLU}[activation]
         return Ops.Linear(x, w, b, epi, gate, residual)
 
     @staticmethod

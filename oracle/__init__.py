@@ -536,3 +536,99 @@ def sdxl_unet(sample, time, add, context, w: dict, cfg):
             x = conv2d(up, w[f"{prefix}.upsamplers.0.conv.weight"], w[f"{prefix}.upsamplers.0.conv.bias"], 1, 1)
     x = group_norm(x, cfg.groups, w["conv_norm_out.weight"], w["conv_norm_out.bias"], cfg.eps, silu=True)
     return conv2d(x, w["conv_out.weight"], w["conv_out.bias"], 1, 1)
+
+
+# ---- Qwen-Image 2.1 (Models/QwenImage/QwenImageDit.cs) -------------------------------
+
+def qwen_pairs_to_halves(w, head_dim):
+    """QwenImageDit.PairsToHalves, QwenImageDit.cs:277-292, row by row: row r
+    = (head, feature) takes source row head*d + 2f (f < d/2) or
+    head*d + 2(f - d/2) + 1 (f >= d/2); a vector is one column."""
+    w = _f32(w)
+    rows = w.shape[0]
+    half = head_dim // 2
+    out = np.empty_like(w)
+    for r in range(rows):
+        head, f = divmod(r, head_dim)
+        src = head * head_dim + (2 * f if f < half else 2 * (f - half) + 1)
+        out[r] = w[src]
+    return out
+
+
+def qwen_block(x, mod, w: dict, i, heads, n_img, cos, sin, key_len, text_mask, eps=1e-6):
+    """QwenImageDit.Block + Attention + FeedForward, QwenImageDit.cs:336-428,
+    on the fp32 residual x [N, D] (image rows first). mod [2, 4D]: the
+    shared modulation's noise-level and time-zero rows (scale1, tanh gate1,
+    scale2, tanh gate2), read by the image and the text rows (Rows, :307-315).
+    The query and key projections and norms go through PairsToHalves and are
+    rotated in halves (Transformer.Rotate); the image rows attend over every
+    key under the key length, the text rows over the text keys under the
+    causal table; the feed-forward is SiLU(gate) * up of the fused gate_up
+    (gate rows first)."""
+    x = _f32(x).copy()
+    mod = _f32(mod)
+    D = x.shape[1]
+    d = D // heads
+    p = f"transformer_blocks.{i}"
+
+    def mod_rows(c, t):
+        return np.concatenate([modulate(t[:n_img], None, mod[0, c * D:(c + 1) * D], eps),
+                               modulate(t[n_img:], None, mod[1, c * D:(c + 1) * D], eps)])
+
+    def gate_rows(c):
+        return np.concatenate([np.broadcast_to(mod[0, c * D:(c + 1) * D], (n_img, D)),
+                               np.broadcast_to(mod[1, c * D:(c + 1) * D], (x.shape[0] - n_img, D))])
+
+    h = mod_rows(0, x)
+    q = linear(h, qwen_pairs_to_halves(w[f"{p}.attn.to_q.weight"], d))
+    k = linear(h, qwen_pairs_to_halves(w[f"{p}.attn.to_k.weight"], d))
+    v = linear(h, w[f"{p}.attn.to_v.weight"])
+    q = rms_norm(q.reshape(-1, d), qwen_pairs_to_halves(w[f"{p}.attn.norm_q.weight"], d), eps).reshape(q.shape)
+    k = rms_norm(k.reshape(-1, d), qwen_pairs_to_halves(w[f"{p}.attn.norm_k.weight"], d), eps).reshape(k.shape)
+    q = rope(q, heads, cos, sin)
+    k = rope(k, heads, cos, sin)
+    image = mha(q[None, :n_img], k[None], v[None], heads, mask_kind=1, key_len=int(key_len))[0]
+    text = mha(q[None, n_img:], k[None, n_img:], v[None, n_img:], heads, mask_kind=2,
+               mask=np.asarray(text_mask, np.int32))[0]
+    a = np.concatenate([image, text])
+    x = x + gate_rows(1) * linear(a, w[f"{p}.attn.to_out.0.weight"])
+    h = mod_rows(2, x)
+    gu = linear(h, w[f"{p}.img_mlp.gate_up.weight"])
+    F = gu.shape[1] // 2
+    f = silu(gu[:, :F]) * gu[:, F:]
+    return x + gate_rows(3) * linear(f, w[f"{p}.img_mlp.out.weight"])
+
+
+def qwen_modulation(sigma, w: dict, time_dim, width):
+    """The time path, QwenImageDit.cs:464-478 with Predict :152-166: temb [2,
+    D] of Sinusoid(1000 sigma) and Sinusoid(0); the modulation [2, 4D] with
+    chunks 1 and 3 through tanh."""
+    time = np.stack([sinusoid(np.float32(sigma * 1000.0), time_dim), sinusoid(0.0, time_dim)])
+    temb = linear(silu(linear(time, w["time_text_embed.timestep_embedder.linear_1.weight"])),
+                  w["time_text_embed.timestep_embedder.linear_2.weight"])
+    mod = linear(silu(temb), w["modulation.1.weight"])
+    D = width
+    mod[:, D:2 * D] = tanh(mod[:, D:2 * D])
+    mod[:, 3 * D:4 * D] = tanh(mod[:, 3 * D:4 * D])
+    return temb, mod
+
+
+def qwen_step(latent, sigma, context, text_mask, key_len, w: dict, blocks, heads, cos, sin, time_dim=256, eps=1e-6):
+    """QwenImageDit.Build + Predict, QwenImageDit.cs:152-166, 430-505: the
+    latent's cells (ToTokens, patch 1) through img_in; the padded context
+    through the zero-centred RMS norm (stored weight + 1) and in_layer,
+    GELU-tanh, out_layer; the blocks; the final modulated projection of the
+    image rows. latent [C, H, W] -> flow [C, H, W]."""
+    C, H, W = latent.shape
+    n_img = H * W
+    D = w["img_in.weight"].shape[0]
+    image = linear(_f32(latent).reshape(C, n_img).T, w["img_in.weight"])
+    text = rms_norm(context, _f32(w["txt_in.text_norm.weight"]) + np.float32(1.0), eps)
+    text = linear(gelu_tanh(linear(text, w["txt_in.in_layer.weight"])), w["txt_in.out_layer.weight"])
+    x = np.concatenate([image, text])
+    temb, mod = qwen_modulation(sigma, w, time_dim, D)
+    for i in range(blocks):
+        x = qwen_block(x, mod, w, i, heads, n_img, cos, sin, key_len, text_mask, eps)
+    scale = linear(silu(temb[:1]), w["norm_out.linear.weight"])[0]
+    out = linear(modulate(x[:n_img], None, scale, eps), w["proj_out.weight"])
+    return out.T.reshape(C, H, W)

@@ -410,3 +410,146 @@ def test_sdxl_unet_joins_value_then_skip_newest_first():
     exp = conv(group_norm(x, 4, w["conv_norm_out.weight"], w["conv_norm_out.bias"], cfg.eps, True), w["conv_out.weight"],
                w["conv_out.bias"])
     assert close(got, exp)
+
+
+# ---- Qwen-Image 2.1 (QwenImageDit.cs) ----------------------------------------------------
+
+def attend_allowed(q, k, v, heads, allowed):
+    """Softmax attention per head over [T, H*d] with a [T, S] table of the
+    keys each query may read (a masked score gets no weight)."""
+    T, D = q.shape
+    d = D // heads
+    q = q.reshape(T, heads, d).transpose(1, 0, 2)
+    k = k.reshape(-1, heads, d).transpose(1, 0, 2)
+    v = v.reshape(-1, heads, d).transpose(1, 0, 2)
+    s = q @ k.transpose(0, 2, 1) / math.sqrt(d)
+    s = np.where(allowed[None], s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return (p @ v).transpose(1, 0, 2).reshape(T, D)
+
+
+def qwen_block64(x, mod, w, p, heads, n_img, cos, sin, key_len, text_mask, eps=1e-6):
+    """The block with Qwen's own rotary form: adjacent feature pairs (2i,
+    2i + 1) of the unpermuted projections turn by the table's angle i, the
+    form PairsToHalves turns into halves."""
+    x = np.asarray(x, f64)
+    N, D = x.shape
+    d = D // heads
+
+    def rows(c):
+        r = np.empty((N, D))
+        r[:n_img], r[n_img:] = mod[0, c * D:(c + 1) * D], mod[1, c * D:(c + 1) * D]
+        return r
+
+    def rot_pairs(t):
+        t = t.reshape(N, heads, d)
+        ev, od = t[..., 0::2], t[..., 1::2]
+        c, s = np.asarray(cos, f64)[:, None, :], np.asarray(sin, f64)[:, None, :]
+        out = np.empty_like(t)
+        out[..., 0::2], out[..., 1::2] = ev * c - od * s, od * c + ev * s
+        return out.reshape(N, D)
+
+    h = layer_norm(x, eps=eps) * (1 + rows(0))
+    q = rot_pairs(rms(lin(h, w[f"{p}.attn.to_q.weight"]).reshape(N, heads, d), w[f"{p}.attn.norm_q.weight"], eps))
+    k = rot_pairs(rms(lin(h, w[f"{p}.attn.to_k.weight"]).reshape(N, heads, d), w[f"{p}.attn.norm_k.weight"], eps))
+    v = lin(h, w[f"{p}.attn.to_v.weight"])
+    image = attend_allowed(q[:n_img], k, v, heads, np.broadcast_to(np.arange(N) < key_len, (n_img, N)))
+    text = attend_allowed(q[n_img:], k[n_img:], v[n_img:], heads, np.asarray(text_mask, bool))
+    x = x + rows(1) * lin(np.concatenate([image, text]), w[f"{p}.attn.to_out.0.weight"])
+    gu = lin(layer_norm(x, eps=eps) * (1 + rows(2)), w[f"{p}.img_mlp.gate_up.weight"])
+    F = gu.shape[1] // 2
+    return x + rows(3) * lin(silu(gu[:, :F]) * gu[:, F:], w[f"{p}.img_mlp.out.weight"])
+
+
+def tiny_qwen(seed, blocks=1):
+    from naivediffusion_amd import qwen
+    cfg = qwen.QwenImageConfig(width=256, heads=2, mlp=96, blocks=blocks, latent_channels=8, context_width=24,
+                               time_dim=32)
+    g = np.random.default_rng(seed)
+    w = {}
+    for name, shape in qwen.weight_shapes(cfg).items():
+        if name.endswith(("norm_q.weight", "norm_k.weight")):
+            w[name] = 1 + rnd(g, *shape, s=0.2)
+        elif name == "txt_in.text_norm.weight":
+            w[name] = rnd(g, *shape, s=0.2)
+        else:
+            w[name] = rnd(g, *shape, s=0.08)
+    return cfg, w, g
+
+
+def test_qwen_pairs_to_halves_in_the_product_follow_the_reference_rows():
+    from naivediffusion_amd import qwen
+    g = np.random.default_rng(0)
+    m, v = rnd(g, 3 * 128, 5), rnd(g, 128)
+    assert np.array_equal(qwen.pairs_to_halves(m, 128), oracle.qwen_pairs_to_halves(m, 128))
+    assert np.array_equal(qwen.pairs_to_halves(v, 128), oracle.qwen_pairs_to_halves(v, 128))
+    gu = rnd(g, 2 * 6, 4)
+    il = qwen.interleave_gate_up(gu)
+    assert np.array_equal(il[0::2], gu[:6]) and np.array_equal(il[1::2], gu[6:])
+
+
+def test_qwen_block_against_float64_pair_rotation():
+    """The oracle's block (PairsToHalves, then rotate-half) against a float64
+    block that rotates the reference's adjacent pairs on the unpermuted
+    weights: a wrong permutation, a rotation in the wrong form, a missing
+    tanh gate or a swapped gate / up would all part them."""
+    cfg, w, g = tiny_qwen(1)
+    n_img, n_txt, real = 6, 5, 3
+    N = n_img + n_txt
+    x = rnd(g, N, cfg.width, s=1.0)
+    mod = rnd(g, 2, 4 * cfg.width, s=0.3)
+    mod[:, cfg.width:2 * cfg.width] = np.tanh(mod[:, cfg.width:2 * cfg.width])
+    mod[:, 3 * cfg.width:] = np.tanh(mod[:, 3 * cfg.width:])
+    cos, sin = oracle.qwen_rope_tables(2, 3, real, n_txt)
+    mask = oracle.causal_table(real, n_txt).reshape(n_txt, n_txt)
+    key_len = n_img + real
+    got = oracle.qwen_block(x, mod, w, 0, cfg.heads, n_img, cos, sin, key_len, mask)
+    exp = qwen_block64(x, mod, w, "transformer_blocks.0", cfg.heads, n_img, cos, sin, key_len, mask)
+    assert close(got - x, exp - x)
+    # The image rows are blind to the padding past the key length.
+    x2 = x.copy()
+    x2[n_img + real:] += rnd(g, n_txt - real, cfg.width, s=1.0)
+    got2 = oracle.qwen_block(x2, mod, w, 0, cfg.heads, n_img, cos, sin, key_len, mask)
+    assert np.max(np.abs(got2[:n_img + real] - got[:n_img + real])) < 1e-5
+
+
+def test_qwen_step_against_float64():
+    from naivediffusion_amd import qwen
+    cfg, w, g = tiny_qwen(2, blocks=2)
+    C, H, W, n_txt, real = cfg.latent_channels, 2, 3, 5, 4
+    latent = rnd(g, C, H, W, s=1.0)
+    ctx = np.zeros((n_txt, cfg.context_width), np.float32)
+    ctx[:real] = rnd(g, real, cfg.context_width, s=1.0)
+    cos, sin = oracle.qwen_rope_tables(H, W, real, n_txt)
+    mask = oracle.causal_table(real, n_txt).reshape(n_txt, n_txt)
+    key_len = H * W + real
+    got = oracle.qwen_step(latent, 0.4, ctx, mask, key_len, w, cfg.blocks, cfg.heads, cos, sin, cfg.time_dim)
+    # float64: the embeddings, the time path and the final layer by hand.
+    D = cfg.width
+    image = lin(latent.reshape(C, -1).T, w["img_in.weight"])
+    t = rms(ctx, 1.0 + np.asarray(w["txt_in.text_norm.weight"], f64), 1e-6)
+    u = lin(t, w["txt_in.in_layer.weight"])
+    u = 0.5 * u * (1 + np.tanh(math.sqrt(2 / math.pi) * (u + 0.044715 * u ** 3)))
+    x = np.concatenate([image, lin(u, w["txt_in.out_layer.weight"])])
+
+    def sinus(tv, width):
+        half = width // 2
+        ang = tv * np.exp(-math.log(10000.0) * np.arange(half) / half)
+        return np.concatenate([np.cos(ang), np.sin(ang)])
+
+    time = np.stack([sinus(400.0, cfg.time_dim), sinus(0.0, cfg.time_dim)])
+    temb = lin(silu(lin(time, w["time_text_embed.timestep_embedder.linear_1.weight"])),
+               w["time_text_embed.timestep_embedder.linear_2.weight"])
+    mod = lin(silu(temb), w["modulation.1.weight"])
+    mod[:, D:2 * D], mod[:, 3 * D:] = np.tanh(mod[:, D:2 * D]), np.tanh(mod[:, 3 * D:])
+    for i in range(cfg.blocks):
+        x = qwen_block64(x, mod, w, f"transformer_blocks.{i}", cfg.heads, H * W, cos, sin, key_len, mask)
+    scale = lin(silu(temb[:1]), w["norm_out.linear.weight"])[0]
+    out = lin(layer_norm(x[:H * W], eps=1e-6) * (1 + scale), w["proj_out.weight"])
+    exp = out.T.reshape(C, H, W)
+    assert close(got, exp, 5e-5)
+    # and the product's host inputs are the oracle's
+    c2, s2 = qwen.rope_tables(H, W, real, n_txt)
+    assert np.max(np.abs(c2 - cos)) < 2e-6 and np.max(np.abs(s2 - sin)) < 2e-6
+    assert np.array_equal(qwen.causal_table(real, n_txt), mask)
