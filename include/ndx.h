@@ -310,6 +310,19 @@ NDX_API ndx_status ndx_op_unpatchify(ndx_graph* graph, ndx_value x, int32_t patc
                                      int32_t channels, int32_t height, int32_t width,
                                      int32_t order, ndx_value* out);
 
+/* The sampler's step on the device, so the latent never leaves it (the
+ * reference downloads it every step, Pipeline/GenerationPipeline.cs:578-616):
+ * classifier-free guidance p = uncond + g * (cond - uncond)
+ * (Pipeline/GuidanceStrategy.cs:34-44; p = cond when uncond is NONE), then
+ * the Euler step x + p * (sigma_next - sigma) (Sampling/Schedulers.cs:270-279)
+ * with the flow prediction's derivative, the model output itself
+ * (Sampling/Prediction.cs:83-84). x, uncond, cond: F32 of one shape;
+ * scalars: F32 [>= 3] holding (g, sigma, sigma_next), read on the device so a
+ * new step binds new values without a new graph. Each float operation is
+ * rounded on its own, as the reference's loops are: bit-exact with them. */
+NDX_API ndx_status ndx_op_guided_euler_step(ndx_graph* graph, ndx_value x, ndx_value uncond, ndx_value cond,
+                                            ndx_value scalars, ndx_value* out);
+
 /* ---- compile / run (Dml/DmlCompiledModel.cs, ModelBuilder.Compile/Run) --- */
 /* DmlGraph.Compile + DmlCompiledModel.Initialize, Dml/DmlGraph.cs:58-163,
  * Dml/DmlCompiledModel.cs:66-75: schedule, plan the intermediates into one

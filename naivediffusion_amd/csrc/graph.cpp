@@ -55,7 +55,7 @@ struct GValue {
 
 enum OpKind {
   OP_ELEM, OP_JOIN, OP_LINEAR, OP_GEMM, OP_ATTN, OP_HNR, OP_ROWNORM, OP_GROUPNORM, OP_CONV,
-  OP_UPSAMPLE, OP_PATCH,
+  OP_UPSAMPLE, OP_PATCH, OP_SAMPLE,
   OP_NHWC,  // compile-time only: an NCHW value copied to NHWC for the implicit-GEMM convolution
 };
 
@@ -1015,6 +1015,30 @@ NDX_API ndx_status ndx_op_patchify(ndx_graph* g, ndx_value x, int32_t patch, int
   NDX_CATCH
 }
 
+NDX_API ndx_status ndx_op_guided_euler_step(ndx_graph* g, ndx_value x, ndx_value uncond, ndx_value cond,
+                                           ndx_value scalars, ndx_value* out) {
+  NDX_TRY
+  NEED(g);
+  NEED(out);
+  GValue& vx = g->val(x);
+  GValue& vc = g->val(cond);
+  GValue& vs = g->val(scalars);
+  if (vx.dtype != NDX_F32 || vc.dtype != NDX_F32 || vs.dtype != NDX_F32)
+    fail(NDX_INVALID_ARG, "the sample, the predictions and the scalars are Float32");
+  if (numel4(vs.v) < 3) fail(NDX_INVALID_ARG, "the scalars are (guidance, sigma, sigma_next)");
+  if (!same_shape(vx.v, vc.v)) fail(NDX_INVALID_ARG, "the prediction " + shape_str(vc.v, vc.dtype) + " is not the sample's shape");
+  if (uncond != NDX_NONE) {
+    GValue& vu = g->val(uncond);
+    if (vu.dtype != NDX_F32 || !same_shape(vx.v, vu.v))
+      fail(NDX_INVALID_ARG, "the unconditional prediction is not the sample's Float32 shape");
+  }
+  GNode n;
+  n.op = OP_SAMPLE;
+  n.in = {x, uncond, cond, scalars};
+  *out = g->emit(n, NDX_F32, vx.v.size, vx.rank);
+  NDX_CATCH
+}
+
 NDX_API ndx_status ndx_op_unpatchify(ndx_graph* g, ndx_value x, int32_t patch, int32_t channels, int32_t height,
                                      int32_t width, int32_t order, ndx_value* out) {
   NDX_TRY
@@ -1189,7 +1213,8 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
       for (int id : n.in) b += bytes_of(id);
       n.bytes = b;
       static const char* names[] = {"elementwise", "join", "linear", "gemm", "attention", "head_norm_rotate",
-                                    "row_norm", "group_norm", "conv2d", "upsample", "patchify"};
+                                    "row_norm", "group_norm", "conv2d", "upsample", "patchify", "guided_euler"};
+      static_assert(sizeof(names) / sizeof(names[0]) == OP_SAMPLE + 1, "a kernel family name per operator");
       n.family = names[n.op];
       if (n.op == OP_ROWNORM) n.family = n.i0 == 0 ? "layer_norm" : n.i0 == 1 ? "modulate" : "rms_norm";
     }
@@ -1481,6 +1506,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         break;
       }
       case OP_PATCH:
+      case OP_SAMPLE:
         for (auto& id : n.in)
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
         break;
@@ -2033,6 +2059,10 @@ struct Runner {
         launch_upsample(a, s);
         break;
       }
+      case OP_SAMPLE:
+        launch_guided_euler((const float*)ptr(n.in[0]), (const float*)ptr(n.in[1]), (const float*)ptr(n.in[2]),
+                            (const float*)ptr(n.in[3]), (float*)ptr(n.out), numel4(val(n.out).v), s);
+        break;
       case OP_PATCH: {
         PatchArgs a{};
         a.x = ptr(n.in[0]);

@@ -346,4 +346,36 @@ void launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int
   hipLaunchKernelGGL(quantize_kernel, dim3(blocks), dim3(256), 0, s, w, w_dtype, rows, cols, block, s_dtype, q, scales);
 }
 
+// The sampler step with classifier-free guidance, in the reference's float
+// arithmetic: p = u + g * (c - u) (GuidanceStrategy.cs:34-44; p = c with no
+// unconditional branch), then x + p * (sigma_next - sigma) (EulerScheduler.
+// Step, Schedulers.cs:270-279, with FlowPrediction's derivative, the model
+// output itself, Prediction.cs:83-84). Each operation is rounded on its own,
+// as the C# loops round them: no fused multiply-add. The scalars (g, sigma,
+// sigma_next) are read from device memory, so a step changes no launch.
+__global__ void guided_euler_kernel(const float* __restrict__ x, const float* __restrict__ u,
+                                    const float* __restrict__ c, const float* __restrict__ scalars,
+                                    float* __restrict__ out, int64_t n) {
+#pragma clang fp contract(off)
+  const float g = scalars[0];
+  const float delta = scalars[2] - scalars[1];
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    float p = c[i];
+    if (u) {
+      const float diff = p - u[i];
+      const float scaled = g * diff;
+      p = u[i] + scaled;
+    }
+    const float step = p * delta;
+    out[i] = x[i] + step;
+  }
+}
+
+void launch_guided_euler(const float* x, const float* u, const float* c, const float* scalars, float* out, int64_t n,
+                         hipStream_t s) {
+  if (n == 0) return;
+  const int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(guided_euler_kernel, dim3(blocks), dim3(256), 0, s, x, u, c, scalars, out, n);
+}
+
 }  // namespace ndx

@@ -220,6 +220,8 @@ const char* conv_family(const ConvArgs& a);
 void launch_elementwise(const ElemArgs& a, hipStream_t s);
 void launch_upsample(const UpsampleArgs& a, hipStream_t s);
 void launch_patch(const PatchArgs& a, hipStream_t s);
+void launch_guided_euler(const float* x, const float* u, const float* c, const float* scalars, float* out, int64_t n,
+                         hipStream_t s);
 void launch_fill_normal(void* ptr, int dtype, int64_t n, uint64_t seed, float mean, float std,
                         hipStream_t s);
 void launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int block,

@@ -312,6 +312,13 @@ class Ops:
         return g._new("ndx_op_group_norm", x.id, _id(weight), _id(bias), int(groups), float(epsilon), int(silu))
 
     @staticmethod
+    def GuidedEulerStep(x, uncond, cond, scalars):
+        """ndx_op_guided_euler_step: x + (u + g (c - u)) (sigma_next - sigma),
+        scalars = (g, sigma, sigma_next); uncond may be None (no guidance)."""
+        g = Ops._same_graph(x, uncond, cond, scalars)
+        return g._new("ndx_op_guided_euler_step", x.id, _id(uncond), cond.id, scalars.id)
+
+    @staticmethod
     def Patchify(x, patch, order=PATCH_CHANNEL_FIRST):
         return x.graph._new("ndx_op_patchify", x.id, int(patch), int(order))
 

@@ -632,3 +632,54 @@ def qwen_step(latent, sigma, context, text_mask, key_len, w: dict, blocks, heads
     scale = linear(silu(temb[:1]), w["norm_out.linear.weight"])[0]
     out = linear(modulate(x[:n_img], None, scale, eps), w["proj_out.weight"])
     return out.T.reshape(C, H, W)
+
+
+# ---- the sampler around the denoiser (Pipeline/, Sampling/) ----------------------------
+
+def cfg_combine(uncond, cond, guidance):
+    """ClassifierFreeGuidance.Combine, Pipeline/GuidanceStrategy.cs:34-44:
+    uncond + g * (cond - uncond), every operation in float32."""
+    u, c = _f32(uncond), _f32(cond)
+    return (u + np.float32(guidance) * (c - u)).astype(np.float32)
+
+
+def euler_step(sample, prediction, sigma, sigma_next):
+    """EulerScheduler.Step, Sampling/Schedulers.cs:270-279, with the flow
+    prediction's derivative (the model output, Prediction.cs:83-84): sample +
+    derivative * (sigma_next - sigma), the difference taken in float32 as the
+    float[] sigmas give it."""
+    delta = np.float32(np.float32(sigma_next) - np.float32(sigma))
+    return (_f32(sample) + _f32(prediction) * delta).astype(np.float32)
+
+
+def mmdit_step(latent, text, t, w: dict, blocks, heads, cos, sin, patch=2, eps=1e-6):
+    """The dual-stream MMDiT denoiser step composed from the primitives above
+    in the order of QwenImageDit's Build (QwenImageDit.cs:430-505): 2x2
+    patchify and img_in, the RMS-normed text through txt_in, the time MLP on
+    Sinusoid(1000 t), the blocks, the final layer (scale, shift) and
+    unpatchify. latent [1, C, H, W], text [Nt, text_dim]; weights by the
+    build's names (blocks.{i}.{img,txt}_*)."""
+    _, C, H, W = latent.shape
+    D = w["img_in.weight"].shape[0]
+    p = patch
+    tokens = _f32(latent)[0].reshape(C, H // p, p, W // p, p).transpose(1, 3, 0, 2, 4).reshape(-1, C * p * p)
+    x_img = linear(tokens, w["img_in.weight"], w["img_in.bias"])
+    x_txt = linear(rms_norm(_f32(text).reshape(-1, w["txt_in.weight"].shape[1]), w["txt_norm.weight"], eps),
+                   w["txt_in.weight"], w["txt_in.bias"])
+    ts = sinusoid(np.float32(t * 1000.0), w["time.linear_1.weight"].shape[1])
+    temb = linear(silu(linear(ts, w["time.linear_1.weight"], w["time.linear_1.bias"])), w["time.linear_2.weight"],
+                  w["time.linear_2.bias"])
+
+    def stream(i, s):
+        q = f"blocks.{i}.{s}"
+        return dict(w_mod=w[f"{q}_mod.weight"], b_mod=w[f"{q}_mod.bias"], w_qkv=w[f"{q}_qkv.weight"],
+                    b_qkv=w[f"{q}_qkv.bias"], norm_q=w[f"{q}_norm_q.weight"], norm_k=w[f"{q}_norm_k.weight"],
+                    w_o=w[f"{q}_out.weight"], b_o=w[f"{q}_out.bias"], w_fc1=w[f"{q}_fc1.weight"],
+                    b_fc1=w[f"{q}_fc1.bias"], w_fc2=w[f"{q}_fc2.weight"], b_fc2=w[f"{q}_fc2.bias"])
+
+    for i in range(blocks):
+        x_img, x_txt = mmdit_block(x_img, x_txt, temb, stream(i, "img"), stream(i, "txt"), heads, cos, sin, -1, eps)
+    mod = linear(silu(temb), w["norm_out.weight"], w["norm_out.bias"])
+    y = modulate(x_img, mod[D:], mod[:D], eps)
+    out = linear(y, w["proj_out.weight"], w["proj_out.bias"])
+    return out.reshape(H // p, W // p, C, p, p).transpose(2, 0, 3, 1, 4).reshape(1, C, H, W)

@@ -135,24 +135,10 @@ TINY = mmdit.MmditConfig(width=256, heads=2, mlp=512, blocks=2, latent_channels=
 
 
 def oracle_step(cfg, w, latent, text, t, cos, sin):
-    """The step composed from oracle primitives, mirroring the reference's
-    Build (QwenImageDit.cs:430-505) with the dual-stream blocks."""
-    C, p, D = cfg.latent_channels, cfg.patch, cfg.width
-    _, _, H, W = latent.shape
-    tokens = latent[0].reshape(C, H // p, p, W // p, p).transpose(1, 3, 0, 2, 4).reshape(-1, C * p * p)
-    x_img = oracle.linear(tokens, w["img_in.weight"], w["img_in.bias"])
-    x_txt = oracle.linear(oracle.rms_norm(text.reshape(-1, cfg.text_dim), w["txt_norm.weight"], cfg.eps),
-                          w["txt_in.weight"], w["txt_in.bias"])
-    ts = oracle.sinusoid(np.float32(t * 1000.0), cfg.time_dim)
-    temb = oracle.linear(oracle.silu(oracle.linear(ts, w["time.linear_1.weight"], w["time.linear_1.bias"])),
-                         w["time.linear_2.weight"], w["time.linear_2.bias"])
-    for i in range(cfg.blocks):
-        x_img, x_txt = oracle.mmdit_block(x_img, x_txt, temb, stream_weights(w, i, "img"),
-                                          stream_weights(w, i, "txt"), cfg.heads, cos, sin, -1, cfg.eps)
-    mod = oracle.linear(oracle.silu(temb), w["norm_out.weight"], w["norm_out.bias"])
-    y = oracle.modulate(x_img, mod[D:], mod[:D], cfg.eps)
-    out = oracle.linear(y, w["proj_out.weight"], w["proj_out.bias"])
-    return out.reshape(H // p, W // p, C, p, p).transpose(2, 0, 3, 1, 4).reshape(1, C, H, W)
+    """The step composed from oracle primitives (oracle.mmdit_step), mirroring
+    the reference's Build (QwenImageDit.cs:430-505) with the dual-stream
+    blocks."""
+    return oracle.mmdit_step(latent, text, t, w, cfg.blocks, cfg.heads, cos, sin, cfg.patch, cfg.eps)
 
 
 @pytest.mark.parametrize("compute,tol", [(DT.BFloat16, 2e-2), (DT.Float32, 1e-3)])
