@@ -59,6 +59,7 @@ typedef struct ndx_device ndx_device;
 typedef struct ndx_tensor ndx_tensor;
 typedef struct ndx_graph ndx_graph;
 typedef struct ndx_model ndx_model;
+typedef struct ndx_safetensors ndx_safetensors;
 
 /* A value (expression) inside one graph; NDX_NONE marks an absent optional
  * operand (the nulls of DmlGraph.Emit, Dml/DmlGraph.cs:38-53). */
@@ -385,6 +386,66 @@ NDX_API ndx_status ndx_model_profile_entry(ndx_model* model, int32_t index, char
                                            double* flops, double* bytes);
 /* DmlCompiledModel.Dispose, Dml/DmlCompiledModel.cs:233. */
 NDX_API ndx_status ndx_model_release(ndx_model* model);
+
+/* ---- checkpoint files and LoRA folding ------------------------------------
+ *
+ * SafetensorsFile (Weights/SafetensorsFile.cs:22-259): the file is mapped
+ * read-only and its header parsed and checked once, at open; every offset is
+ * checked against the file before anything reads there. A refused file is
+ * unmapped before open returns. Strings and mapped bytes handed out stay
+ * valid until ndx_safetensors_close. */
+
+/* The constructor (:35-66) and ReadHeader (:70-149). NDX_INVALID_ARG with the
+ * reference's reasons: too short, a header that does not fit the file, JSON
+ * that does not parse, JSON that is not a tensor table, an entry pointing
+ * outside the file. */
+NDX_API ndx_status ndx_safetensors_open(const char* path, ndx_safetensors** out);
+/* Dispose (:198-214). NULL is allowed. */
+NDX_API ndx_status ndx_safetensors_close(ndx_safetensors* file);
+/* How many tensor entries and string-valued __metadata__ notes the header has. */
+NDX_API ndx_status ndx_safetensors_count(ndx_safetensors* file, int32_t* entries, int32_t* metadata);
+/* Keys and TryGetInfo (:151-169): entry index's name, dtype as written (which
+ * may be one ndx_safetensors_read refuses), shape (up to 8 axes), rank and
+ * byte length. Any output may be NULL. */
+NDX_API ndx_status ndx_safetensors_entry(ndx_safetensors* file, int32_t index, const char** name,
+                                         const char** dtype, int64_t* shape, int32_t* rank, uint64_t* bytes);
+/* Metadata (:151-155): note index's key and value. */
+NDX_API ndx_status ndx_safetensors_metadata(ndx_safetensors* file, int32_t index, const char** key,
+                                            const char** value);
+/* Read's window (:172-180): the mapped bytes of a tensor, no copy. */
+NDX_API ndx_status ndx_safetensors_data(ndx_safetensors* file, const char* name, const void** data,
+                                        uint64_t* bytes);
+/* Read (:172-180) straight into device memory, narrowed on the way as
+ * LazyWeights narrows (Weights/LazyWeights.cs:39-48, HostTensor.ConvertTo):
+ * the bytes go from the mapping through pinned staging buffers to the device
+ * and a float tensor is converted there to dtype (a float type; -1 keeps the
+ * stored type), rounding to nearest even. A dtype IsSupportedDataType
+ * (:229-240) refuses is NDX_UNSUPPORTED ("safetensors dtype X is not
+ * supported"). More than 4 axes are folded into the first. Returns when the
+ * tensor is on the device. */
+NDX_API ndx_status ndx_safetensors_read(ndx_safetensors* file, const char* name, ndx_device* device,
+                                        int32_t dtype, ndx_tensor** out);
+
+/* One LoRA pair to fold: down is [rank, the weight's row length] (trailing
+ * axes of a convolution flattened), up is [rows covered, rank], added from
+ * row first_row on with factor scale (weight * alpha / rank,
+ * Weights/LoraFile.cs:492). */
+typedef struct ndx_lora_patch {
+    const ndx_tensor* down;
+    const ndx_tensor* up;
+    float scale;
+    int32_t first_row;
+} ndx_lora_patch;
+#define NDX_MAX_LORA_PATCHES 16
+/* LoraMerge.Merge (Weights/LoraFile.cs:355-420) on the device: a new tensor
+ * of the weight's shape, each row widened to float32, given
+ * (scale * up[row, r]) * down[r, :] for every pair covering it (in order) and
+ * every rank r in order, each product and sum rounded on its own, zero
+ * factors skipped, then narrowed once to dtype (-1: the reference's width,
+ * Float32 for a Float32 weight, else Float16). Up to NDX_MAX_LORA_PATCHES
+ * pairs; the pairs' matrices may be any float type. */
+NDX_API ndx_status ndx_lora_fold(const ndx_tensor* weight, const ndx_lora_patch* patches, int32_t count,
+                                 int32_t dtype, ndx_tensor** out);
 
 #ifdef __cplusplus
 }

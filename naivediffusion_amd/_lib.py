@@ -118,7 +118,23 @@ SIGNATURES = [
     ("ndx_model_set_profile_filter", i32, [vp, ctypes.c_char_p]),
     ("ndx_model_profile_entry", i32, [vp, i32, ctypes.c_char_p, i32, P(i64), P(f64), P(f64), P(f64)]),
     ("ndx_model_release", i32, [vp]),
+    ("ndx_safetensors_open", i32, [cstr, P(vp)]),
+    ("ndx_safetensors_close", i32, [vp]),
+    ("ndx_safetensors_count", i32, [vp, P(i32), P(i32)]),
+    ("ndx_safetensors_entry", i32, [vp, i32, P(cstr), P(cstr), P(i64), P(i32), P(u64)]),
+    ("ndx_safetensors_metadata", i32, [vp, i32, P(cstr), P(cstr)]),
+    ("ndx_safetensors_data", i32, [vp, cstr, P(vp), P(u64)]),
+    ("ndx_safetensors_read", i32, [vp, cstr, vp, i32, P(vp)]),
+    ("ndx_lora_fold", i32, [vp, vp, i32, i32, P(vp)]),
 ]
+
+
+class LoraPatch(ctypes.Structure):
+    """ndx_lora_patch."""
+    _fields_ = [("down", vp), ("up", vp), ("scale", f32), ("first_row", i32)]
+
+
+MAX_LORA_PATCHES = 16  # NDX_MAX_LORA_PATCHES
 
 _lib = None
 

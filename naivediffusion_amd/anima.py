@@ -357,3 +357,19 @@ class AnimaDit:
 
     def Dispose(self):
         self.chain.Dispose()
+
+
+# ---- LoRAs (Models/Anima/AnimaLoras.cs) ----------------------------------------------------
+
+LORA_DIT, LORA_TEXT_ENCODER = "dit", "te"
+
+
+def lora_layout():
+    """AnimaLoras.Layout (AnimaLoras.cs:14-31): the transformer as
+    lora_unet_... or diffusion_model..., the Qwen3 encoder as lora_te_... or
+    text_encoders...; SDXL's two text towers refused on their names."""
+    from .lora import LoraLayout, LoraTower
+    sdxl = "was trained for SDXL, whose text encoders are two CLIP towers where Anima has Qwen3"
+    return LoraLayout("Anima", [LoraTower(LORA_DIT, "transformer", "unet", "diffusion_model"),
+                                LoraTower(LORA_TEXT_ENCODER, "Qwen3 text encoder", "te", "text_encoders")],
+                      {"te1": sdxl, "te2": sdxl})

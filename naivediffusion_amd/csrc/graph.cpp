@@ -263,22 +263,6 @@ int make_elem(ndx_graph* g, int op, int a, int b, int out_dtype, float scale = 1
 
 }  // namespace
 
-#define NDX_TRY try {
-#define NDX_CATCH                            \
-  }                                          \
-  catch (const ndx::Error& e) {              \
-    ndx::set_last_error(e.message);          \
-    return e.status;                         \
-  }                                          \
-  catch (const std::exception& e) {          \
-    ndx::set_last_error(e.what());           \
-    return NDX_INVALID_STATE;                \
-  }                                          \
-  return NDX_OK;
-
-#define NEED(x) \
-  if (!(x)) fail(NDX_INVALID_ARG, #x " is null")
-
 extern "C" {
 
 NDX_API ndx_status ndx_graph_create(ndx_device* device, int32_t dtype, int32_t int8_weights,

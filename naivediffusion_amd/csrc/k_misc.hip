@@ -378,4 +378,51 @@ void launch_guided_euler(const float* x, const float* u, const float* c, const f
   hipLaunchKernelGGL(guided_euler_kernel, dim3(blocks), dim3(256), 0, s, x, u, c, scalars, out, n);
 }
 
+// LoRA fold (LoraMerge.Merge, Weights/LoraFile.cs:355-420). A thread owns
+// one column of ROWS consecutive rows and keeps them widened to fp32 in
+// registers; for each pair covering a row and each rank r in order it adds
+// (scale * up[row - first, r]) * down[r, col], the product and the sum each
+// rounded on their own as the C# vector multiply-add rounds them, and skips a
+// zero factor as the reference does; the row is narrowed once at the end.
+// A block reads each down row once for its ROWS rows; the up factors are the
+// same for every lane, so they come through the scalar unit.
+template <int ROWS>
+__global__ __launch_bounds__(256) void lora_fold_kernel(LoraFoldArgs a) {
+#pragma clang fp contract(off)
+  const int64_t col = int64_t(blockIdx.y) * 256 + threadIdx.x;
+  const int64_t r0 = int64_t(blockIdx.x) * ROWS;
+  if (col >= a.cols) return;
+  const int live = (int)min<int64_t>(ROWS, a.rows - r0);
+  float acc[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) acc[i] = i < live ? load_f(a.w, a.w_dtype, (r0 + i) * a.cols + col) : 0.f;
+  for (int k = 0; k < a.patches; k++) {
+    const LoraPatchArgs& p = a.p[k];
+    if (r0 + live <= p.first || r0 >= p.first + p.count) continue;
+    for (int r = 0; r < p.rank; r++) {
+      const float d = load_f(p.down, p.down_dtype, int64_t(r) * a.cols + col);
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const int64_t row = r0 + i;
+        if (i >= live || row < p.first || row >= p.first + p.count) continue;
+        const float factor = p.scale * load_f(p.up, p.up_dtype, (row - p.first) * p.rank + r);
+        if (factor == 0.f) continue;
+        const float term = d * factor;
+        acc[i] = term + acc[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < ROWS; i++)
+    if (i < live) store_f(a.out, a.out_dtype, (r0 + i) * a.cols + col, acc[i]);
+}
+
+void launch_lora_fold(const LoraFoldArgs& a, hipStream_t s) {
+  if (a.rows == 0 || a.cols == 0) return;
+  constexpr int R = 16;
+  // Row groups on x (up to 2^31 of them), column groups on y.
+  const dim3 grid((unsigned)((a.rows + R - 1) / R), (unsigned)((a.cols + 255) / 256));
+  hipLaunchKernelGGL(lora_fold_kernel<R>, grid, dim3(256), 0, s, a);
+}
+
 }  // namespace ndx

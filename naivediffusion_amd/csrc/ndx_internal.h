@@ -37,6 +37,28 @@ void set_last_error(const std::string& message);
 // Checks a HIP call; out-of-memory becomes NDX_OOM, anything else DEVICE_LOST.
 void hip_check(hipError_t err, const char* what);
 
+}  // namespace ndx
+
+// The body of every C entry point: library errors become the returned status
+// and ndx_last_error's message.
+#define NDX_TRY try {
+#define NDX_CATCH                   \
+  }                                 \
+  catch (const ndx::Error& e) {     \
+    ndx::set_last_error(e.message); \
+    return e.status;                \
+  }                                 \
+  catch (const std::exception& e) { \
+    ndx::set_last_error(e.what());  \
+    return NDX_INVALID_STATE;       \
+  }                                 \
+  return NDX_OK;
+
+#define NEED(x) \
+  if (!(x)) ndx::fail(NDX_INVALID_ARG, #x " is null")
+
+namespace ndx {
+
 // ---- strided 4-D views -----------------------------------------------------
 
 // Every tensor inside the library is a 4-D view: sizes outermost first,
@@ -231,6 +253,27 @@ void launch_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols, int
 // graph's ModelBuilder.Weight path.
 void quantize_host(const void* w, int dtype, int64_t rows, int64_t cols, int block, int s_dtype,
                    int8_t* q, void* scales);
+
+// A LoRA's low-rank pairs folded into a weight (LoraMerge.Merge): each
+// output row is widened to fp32, takes scale * up[row - first, r] * down[r, :]
+// for every pair covering it, rank by rank, and is narrowed once.
+constexpr int kMaxLoraPatches = NDX_MAX_LORA_PATCHES;
+struct LoraPatchArgs {
+  const void* down;  // [rank, cols]
+  const void* up;    // [count, rank]
+  int down_dtype, up_dtype;
+  int rank;
+  int64_t first, count;
+  float scale;
+};
+struct LoraFoldArgs {
+  const void* w; int w_dtype;
+  void* out; int out_dtype;
+  int64_t rows, cols;
+  int patches;
+  LoraPatchArgs p[kMaxLoraPatches];
+};
+void launch_lora_fold(const LoraFoldArgs& a, hipStream_t s);
 
 // Which GEMM kernel a shape goes to, and the algorithmic work, for profiling.
 const char* gemm_family(const GemmArgs& a);

@@ -219,19 +219,6 @@ void ndx_device::check_usable() const {
   if (lost || fault == 2) fail(NDX_DEVICE_LOST, "the device was lost");
 }
 
-#define NDX_TRY try {
-#define NDX_CATCH                                                   \
-  }                                                                 \
-  catch (const ndx::Error& e) {                                     \
-    ndx::set_last_error(e.message);                                 \
-    return e.status;                                                \
-  }                                                                 \
-  catch (const std::exception& e) {                                 \
-    ndx::set_last_error(e.what());                                  \
-    return NDX_INVALID_STATE;                                       \
-  }                                                                 \
-  return NDX_OK;
-
 static void mark_lost_on(ndx_device* dev, const ndx::Error& e) {
   if (dev && e.status == NDX_DEVICE_LOST) dev->lost = true;
 }

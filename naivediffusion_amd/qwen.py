@@ -40,6 +40,12 @@ from .graph import CompiledModel, Graph, MaskType, ModelBuilder, Ops
 from .layers import Layers, Transformer
 from .tensors import Device, DeviceTensor, HostDataType, HostTensor, bf16_to_f32, f32_to_bf16
 
+# QwenImageCheckpoint's names for the feed-forward's first projection
+# (Models/QwenImage/QwenImageCheckpoint.cs:32-34).
+FUSED_GATE_UP = "img_mlp.gate_up.weight"
+GATE_PROJECTION = "img_mlp.gate_layer.weight"
+UP_PROJECTION = "img_mlp.proj.weight"
+
 ROPE_AXES = (16, 56, 56)
 ROPE_THETA = 10000.0
 F32 = HostDataType.Float32
@@ -217,6 +223,16 @@ def _pairs_device(w: DeviceTensor, head_dim: int) -> DeviceTensor:
     return _device_view_copy(w.Device, w, [heads, 2, half, cols], [head_dim * cols, cols, 2 * cols, 1], shape)
 
 
+def _gate_up(weights, p: str):
+    """The block's [gate; up] projection: the fused matrix as Comfy-Org saves
+    it, or diffusers' two matrices stacked (QwenImageDit.FeedForward,
+    :390-406)."""
+    fused = f"{p}.{FUSED_GATE_UP}"
+    if fused in weights:
+        return weights[fused]
+    return _stack([weights[f"{p}.{GATE_PROJECTION}"], weights[f"{p}.{UP_PROJECTION}"]])
+
+
 def interleave_gate_up(w):
     """The fused [2F, D] gate-then-up projection with its rows interleaved
     (row 2j the gate's j, row 2j + 1 the up's j): what the SwiGLU epilogue
@@ -322,8 +338,8 @@ def build_block(model: ModelBuilder, W: _Weights, i: int, cfg: QwenImageConfig, 
     x = Layers.Linear(model, attended, W(f"{p}.attn.to_out.0.weight"), gate=rows(modulation, 1, D, n_img, n_txt),
                       residual=x)
     normed = Transformer.Modulate(x, rows(modulation, 2, D, n_img, n_txt), eps, compute)
-    f = Layers.Linear(model, normed, W.derived(f"{p}.gate_up", lambda: interleave_gate_up(
-        W.weights[f"{p}.img_mlp.gate_up.weight"])), activation="swiglu")
+    f = Layers.Linear(model, normed, W.derived(f"{p}.gate_up", lambda: interleave_gate_up(_gate_up(W.weights, p))),
+                      activation="swiglu")
     return Layers.Linear(model, f, W(f"{p}.img_mlp.out.weight"), gate=rows(modulation, 3, D, n_img, n_txt),
                          residual=x)
 
@@ -447,3 +463,96 @@ class QwenImageDit:
 
     def Dispose(self):
         self.model.Dispose()
+
+
+# ---- checkpoints and LoRAs (QwenImageCheckpoint.cs, QwenImageLoras.cs, QwenImageWeights.cs) ---
+
+DIT_PREFIXES = ("", "model.diffusion_model.")
+# The tensors that together mark Qwen-Image 2.1's transformer
+# (QwenImageCheckpoint.cs:24-28).
+DIT_MARKERS = ("txt_in.text_norm.weight", "modulation.1.weight", "transformer_blocks.0.attn.norm_q.weight",
+               "img_in.weight", "proj_out.weight")
+
+
+def dit_prefix(file) -> "str | None":
+    """QwenImageCheckpoint.DitPrefix (:38-50): the prefix the transformer
+    sits under in a SafetensorsFile, or None for another file."""
+    keys = set(file.Keys)
+    for prefix in DIT_PREFIXES:
+        if all(prefix + m in keys for m in DIT_MARKERS) and (
+                f"{prefix}transformer_blocks.0.{FUSED_GATE_UP}" in keys
+                or f"{prefix}transformer_blocks.0.{GATE_PROJECTION}" in keys):
+            return prefix
+    return None
+
+
+def config_from_shapes(shapes: Dict[str, tuple]) -> QwenImageConfig:
+    """The model's widths from its weights' shapes, as the reference's
+    constructor reads them (QwenImageDit.cs:119-144): width and latent
+    channels from img_in, the head from the query norm, the feed-forward
+    from the gate rows, the time width from linear_1, the blocks by count and
+    the context width from the text norm (QwenImageDit.ContextWidth)."""
+    from .safetensors import InvalidDataError
+    emb = tuple(shapes["img_in.weight"])
+    if len(emb) != 2:
+        raise InvalidDataError(f"img_in.weight is [{', '.join(map(str, emb))}], not [width, channels]")
+    width, channels = emb
+    head = shapes["transformer_blocks.0.attn.norm_q.weight"][0]
+    if head != sum(ROPE_AXES) or width % head:
+        raise InvalidDataError(f"a head of {head} features does not take the rotary axes")
+    fused = f"transformer_blocks.0.{FUSED_GATE_UP}"
+    mlp = shapes[fused][0] // 2 if fused in shapes else shapes[f"transformer_blocks.0.{GATE_PROJECTION}"][0]
+    blocks = 0
+    while f"transformer_blocks.{blocks}.attn.to_q.weight" in shapes:
+        blocks += 1
+    norm = tuple(shapes["txt_in.text_norm.weight"])
+    if len(norm) != 1:
+        raise InvalidDataError("the text norm has an unexpected shape")
+    return QwenImageConfig(width=width, heads=width // head, mlp=mlp, blocks=blocks, latent_channels=channels,
+                           context_width=norm[0],
+                           time_dim=shapes["time_text_embed.timestep_embedder.linear_1.weight"][1])
+
+
+LORA_DIT = "dit"
+LORA_TEXT_ENCODER = "te"
+
+
+def lora_layout():
+    """QwenImageLoras.Layout (QwenImageLoras.cs:19-33): the transformer as
+    kohya's lora_unet_..., diffusion_model..., transformer... or bare names,
+    the Qwen3-VL text encoder as lora_te_... or text_encoders...; SDXL's two
+    text towers refused on their names."""
+    from .lora import LoraLayout, LoraTower
+    sdxl = "was trained for SDXL, whose text encoders are two CLIP towers where Qwen-Image has Qwen3-VL"
+    return LoraLayout("Qwen-Image 2.1",
+                      [LoraTower(LORA_DIT, "transformer", "unet", "diffusion_model", ("transformer", "")),
+                       LoraTower(LORA_TEXT_ENCODER, "Qwen3-VL text encoder", "te", "text_encoders")],
+                      {"te1": sdxl, "te2": sdxl})
+
+
+def fused_halves(key: str, rows: int):
+    """QwenImageLoras.FusedHalves (:39-49): the names a LoRA has for the two
+    halves of the fused gate/up matrix."""
+    from .lora import LoraRows
+    if not key.endswith("." + FUSED_GATE_UP):
+        return []
+    block = key[: -len(FUSED_GATE_UP)]
+    return [LoraRows(block + GATE_PROJECTION, 0, rows // 2), LoraRows(block + UP_PROJECTION, rows // 2, rows // 2)]
+
+
+def load_dit(file, device: Device, loras=(), dtype: HostDataType = HostDataType.BFloat16):
+    """QwenImageWeights.LoadDit (QwenImageWeights.cs:26-34) for the device:
+    the transformer's tensors under their bare names, each read from the
+    mapping into HBM when the builder asks for it, narrowed there to dtype,
+    with the LoRAs' deltas folded in on the device. A LoRA that fits nothing
+    is refused here, before the build starts. Returns (config, weights)."""
+    from .lora import LazyWeights, LoraPatchSet
+    from .safetensors import InvalidDataError
+    prefix = dit_prefix(file)
+    if prefix is None:
+        raise InvalidDataError("not a Qwen-Image 2.1 checkpoint")
+    shapes = {k[len(prefix):]: file.TryGetInfo(k)[2] for k in file.Keys if k.startswith(prefix)}
+    patches = (LoraPatchSet.Prepare(shapes, lora_layout(), LORA_DIT, list(loras),
+                                    parts=lambda key: fused_halves(key, shapes[key][0]))
+               if loras else None)
+    return config_from_shapes(shapes), LazyWeights(file, prefix, patches, dtype, device)

@@ -361,3 +361,18 @@ class UNetModel:
 
     def Dispose(self):
         self.model.Dispose()
+
+
+# ---- LoRAs (Models/Sdxl/SdxlLoras.cs) ------------------------------------------------------
+
+LORA_UNET, LORA_TEXT_ENCODER, LORA_TEXT_ENCODER_2 = "unet", "te1", "te2"
+
+
+def lora_layout():
+    """SdxlLoras.Layout (SdxlLoras.cs:11-28): the UNet and the two CLIP
+    towers; a kohya lora_te_ file (one text tower) is refused as SD 1.x/2.x."""
+    from .lora import LoraLayout, LoraTower
+    return LoraLayout("SDXL", [LoraTower(LORA_UNET, "UNet", "unet", "unet"),
+                               LoraTower(LORA_TEXT_ENCODER, "CLIP-L", "te1", "text_encoder"),
+                               LoraTower(LORA_TEXT_ENCODER_2, "CLIP-G", "te2", "text_encoder_2")],
+                      {"te": "was trained for Stable Diffusion 1.x or 2.x, which has one text tower where SDXL has two"})

@@ -50,6 +50,7 @@ def lib():
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.orc_f32_to_bf16.restype = ctypes.c_uint16
         L.orc_f32_to_bf16.argtypes = [c_float]
+        L.orc_lora_merge.argtypes = [_f32p, c_i64, c_i64, _f32p, _f32p, c_int, c_float, c_i64, c_i64]
         L.orc_dot.restype = c_float
         L.orc_dot.argtypes = [_f32p, _f32p, c_int]
         L.orc_linear.argtypes = [_f32p, c_int, c_int, _f32p, vp, vp, c_int]
@@ -683,3 +684,28 @@ def mmdit_step(latent, text, t, w: dict, blocks, heads, cos, sin, patch=2, eps=1
     y = modulate(x_img, mod[D:], mod[:D], eps)
     out = linear(y, w["proj_out.weight"], w["proj_out.bias"])
     return out.reshape(H // p, W // p, C, p, p).transpose(2, 0, 3, 1, 4).reshape(1, C, H, W)
+
+
+def lora_scale(weight, alpha, rank) -> float:
+    """The pair's factor weight * (alpha or rank) / rank in float32, left to
+    right (LoraPatchSet.Prepare, Weights/LoraFile.cs:492)."""
+    a = np.float32(rank if alpha is None else alpha)
+    return float(np.float32(np.float32(np.float32(weight) * a) / np.float32(rank)))
+
+
+def lora_merge(weight, patches):
+    """LoraMerge.Merge (Weights/LoraFile.cs:362-420) through orc_lora_merge:
+    weight is float32 values (a float16 / bfloat16 weight widened exactly),
+    patches a list of (down [rank, cols], up [count, rank], scale, first_row).
+    Returns the merged rows in float32 before narrowing; narrow with
+    f32_to_f16_bits / f32_to_bf16_bits as the reference's width asks."""
+    w = np.array(weight, np.float32, copy=True)
+    rows = w.shape[0]
+    flat = np.ascontiguousarray(w.reshape(rows, -1))
+    cols = flat.shape[1]
+    for down, up, scale, first in patches:
+        down = _f32(np.asarray(down).reshape(-1, cols))
+        rank = down.shape[0]
+        up = _f32(np.asarray(up).reshape(-1, rank))
+        lib().orc_lora_merge(flat, rows, cols, down, up, rank, float(np.float32(scale)), int(first), up.shape[0])
+    return flat.reshape(w.shape)

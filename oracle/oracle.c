@@ -621,3 +621,27 @@ API void orc_mmdit_block(float* x_img, int n_img, float* x_txt, int n_txt, const
     free(f);
     free(o);
 }
+
+/* LoraMerge.Merge (Weights/LoraFile.cs:362-420), one pair: rows holds the
+ * weight widened to float32 ([n_rows, cols]) and is updated in place. For
+ * each covered row (first .. first + count) and each rank r in order, the
+ * factor scale * up[row - first, r] is formed in float32, skipped when it is
+ * zero, and down[r, :] * factor is added to the row, the product and the sum
+ * each rounded (TensorPrimitives.MultiplyAdd, not fused). Several pairs are
+ * applied by calling this once per pair in order: every element sees the
+ * same sequence of operations as in the reference's row loop. */
+API void orc_lora_merge(float* rows, int64_t n_rows, int64_t cols, const float* down, const float* up, int rank,
+                        float scale, int64_t first, int64_t count) {
+    for (int64_t row = first; row < first + count && row < n_rows; row++) {
+        float* acc = rows + (size_t)row * cols;
+        for (int r = 0; r < rank; r++) {
+            const float factor = scale * up[(size_t)(row - first) * rank + r];
+            if (factor == 0.0f) continue;
+            const float* d = down + (size_t)r * cols;
+            for (int64_t c = 0; c < cols; c++) {
+                const float term = d[c] * factor;
+                acc[c] = term + acc[c];
+            }
+        }
+    }
+}
