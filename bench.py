@@ -368,13 +368,36 @@ def setup_sdxl(args, dev, seed, DT):
     )
 
 
+def setup_vae(args, dev, seed, DT):
+    from naivediffusion_amd import rng, vae
+
+    cfg = vae.SDXL
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    side = 1024
+    lat = side // cfg.scale_factor
+    weights = vae.device_weights(dev, cfg, seed, compute)
+    model = vae.build_decoder(dev, cfg, weights, side, side, compute)
+    inputs = [dev.Normal(DT.Float32, [1, cfg.latent_channels, lat, lat], rng.tensor_seed(seed, "latent"), 0.0,
+                         cfg.scaling_factor)]
+    out = [dev.Empty(compute, [1, cfg.image_channels, side, side])]
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="SDXL VAE decode s/image @1024x1024, 1 MI355X; % MFMA peak",
+        config={"workload": (f"SDXL VAE decoder (AutoencoderKL 128/256/512/512), latent 4x{lat}x{lat} -> "
+                             f"3x{side}x{side}, {args.compute} compute"), "batch": 1},
+        data="synthetic (seeded latent, N(0, 1/fan_in) weights made on the GPU)",
+        cpu=None,
+    )
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl", "qwen"], default="mmdit",
-                    help="mmdit (the headline), or the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps")
+    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl", "qwen", "vae"], default="mmdit",
+                    help="mmdit (the headline), or the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps, or the SDXL "
+                         "VAE decode")
     ap.add_argument("--compute", choices=["bf16", "f32", "f16"], default=None,
                     help="compute type (default bf16; fp16 for sdxl)")
     ap.add_argument("--int8", nargs="?", const="block32", default=None, choices=["block32", "channel"],
@@ -409,7 +432,8 @@ def main():
     dev = nd.Device()
     log(f"device {dev.AdapterName}")
     t0 = time.perf_counter()
-    setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl, "qwen": setup_qwen}[args.workload](
+    setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl, "qwen": setup_qwen,
+             "vae": setup_vae}[args.workload](
         args, dev, seed, DT)
     compiled = setup["model"].Compiled
     log(f"graph built and compiled in {time.perf_counter() - t0:.1f} s: {compiled.KernelCount} kernels/step, "

@@ -267,6 +267,10 @@ NDX_API ndx_status ndx_op_attention(ndx_graph* graph, ndx_value q, ndx_value k, 
 NDX_API ndx_status ndx_op_head_norm_rotate(ndx_graph* graph, ndx_value x, ndx_value weight,
                                            float eps, ndx_value cos, ndx_value sin,
                                            int32_t heads, int32_t out_dtype, ndx_value* out);
+/* DmlOps.ActivationSoftmax over the last axis (Dml/DmlOps.cs:175-184) of
+ * scale * x, at x's type; scale folds the alpha of the Gemm that made x
+ * (AutoencoderKl.AttentionBlock, Vae/AutoencoderKl.cs:57-60). */
+NDX_API ndx_status ndx_op_softmax(ndx_graph* graph, ndx_value x, float scale, ndx_value* out);
 /* Layers.LayerNorm(x, eps) and the affine form, Graph/Layers.cs:189-197,
  * 225-226 (MVN1 over the last axis, Dml/DmlOps.cs:305-319). */
 NDX_API ndx_status ndx_op_layer_norm(ndx_graph* graph, ndx_value x, ndx_value weight,

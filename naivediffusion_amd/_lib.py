@@ -107,6 +107,7 @@ SIGNATURES = [
     ("ndx_op_patchify", i32, [vp, i32, i32, i32, P(i32)]),
     ("ndx_op_unpatchify", i32, [vp, i32, i32, i32, i32, i32, i32, P(i32)]),
     ("ndx_op_guided_euler_step", i32, [vp, i32, i32, i32, i32, P(i32)]),
+    ("ndx_op_softmax", i32, [vp, i32, f32, P(i32)]),
     ("ndx_graph_compile", i32, [vp, P(i32), i32, P(vp)]),
     ("ndx_model_sizes", i32, [vp, P(u64), P(u64)]),
     ("ndx_model_counts", i32, [vp, P(i32), P(i32), P(i32)]),

@@ -55,7 +55,7 @@ struct GValue {
 
 enum OpKind {
   OP_ELEM, OP_JOIN, OP_LINEAR, OP_GEMM, OP_ATTN, OP_HNR, OP_ROWNORM, OP_GROUPNORM, OP_CONV,
-  OP_UPSAMPLE, OP_PATCH, OP_SAMPLE,
+  OP_UPSAMPLE, OP_PATCH, OP_SAMPLE, OP_SOFTMAX,
   OP_NHWC,  // compile-time only: an NCHW value copied to NHWC for the implicit-GEMM convolution
 };
 
@@ -1023,6 +1023,21 @@ NDX_API ndx_status ndx_op_guided_euler_step(ndx_graph* g, ndx_value x, ndx_value
   NDX_CATCH
 }
 
+NDX_API ndx_status ndx_op_softmax(ndx_graph* g, ndx_value x, float scale, ndx_value* out) {
+  NDX_TRY
+  NEED(g);
+  NEED(out);
+  GValue& vx = g->val(x);
+  if (vx.dtype != NDX_F32 && vx.dtype != NDX_BF16 && vx.dtype != NDX_F16)
+    fail(NDX_INVALID_ARG, "a softmax reads Float32, Float16 or BFloat16");
+  GNode n;
+  n.op = OP_SOFTMAX;
+  n.in = {x};
+  n.f0 = scale;
+  *out = g->emit(n, vx.dtype, vx.v.size, vx.rank);
+  NDX_CATCH
+}
+
 NDX_API ndx_status ndx_op_unpatchify(ndx_graph* g, ndx_value x, int32_t patch, int32_t channels, int32_t height,
                                      int32_t width, int32_t order, ndx_value* out) {
   NDX_TRY
@@ -1197,8 +1212,9 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
       for (int id : n.in) b += bytes_of(id);
       n.bytes = b;
       static const char* names[] = {"elementwise", "join", "linear", "gemm", "attention", "head_norm_rotate",
-                                    "row_norm", "group_norm", "conv2d", "upsample", "patchify", "guided_euler"};
-      static_assert(sizeof(names) / sizeof(names[0]) == OP_SAMPLE + 1, "a kernel family name per operator");
+                                    "row_norm", "group_norm", "conv2d", "upsample", "patchify", "guided_euler",
+                                    "softmax"};
+      static_assert(sizeof(names) / sizeof(names[0]) == OP_SOFTMAX + 1, "a kernel family name per operator");
       n.family = names[n.op];
       if (n.op == OP_ROWNORM) n.family = n.i0 == 0 ? "layer_norm" : n.i0 == 1 ? "modulate" : "rms_norm";
     }
@@ -1491,6 +1507,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       }
       case OP_PATCH:
       case OP_SAMPLE:
+      case OP_SOFTMAX:
         for (auto& id : n.in)
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
         break;
@@ -2041,6 +2058,12 @@ struct Runner {
         a.H = x.v.size[2];
         a.W = x.v.size[3];
         launch_upsample(a, s);
+        break;
+      }
+      case OP_SOFTMAX: {
+        const View4& o = val(n.out).v;
+        launch_softmax(ptr(n.in[0]), ptr(n.out), val(n.out).dtype, o.size[0] * o.size[1] * o.size[2], o.size[3], n.f0,
+                       s);
         break;
       }
       case OP_SAMPLE:

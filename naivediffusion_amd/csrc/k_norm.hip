@@ -733,4 +733,83 @@ void launch_group_norm(const GroupNormArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(group_norm_apply_kernel, g, dim3(256), 0, s, a);
 }
 
+// Softmax over the last axis (DmlOps.ActivationSoftmax with axes {3},
+// Dml/DmlOps.cs:175-184) of scale * x, written at x's type: one 256-thread
+// workgroup per row. Pass one keeps a running (max, sum of exp) per thread and
+// merges them across the workgroup; pass two reads the row again (from L2: a
+// row is at most a few hundred KB) and writes exp(scale * x - max) / sum.
+// Rows whose length is a multiple of 8 at 16-byte aligned addresses move 8
+// elements per load.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const void* __restrict__ x, void* __restrict__ y,
+                                                           int64_t cols, float scale) {
+  const int64_t base = int64_t(blockIdx.x) * cols;
+  const int tid = threadIdx.x;
+  float m = -INFINITY, sum = 0.f;
+  auto take = [&](float v) {
+    v *= scale;
+    if (v > m) {
+      sum = sum * __expf(m - v) + 1.f;
+      m = v;
+    } else {
+      sum += __expf(v - m);
+    }
+  };
+  if constexpr (VEC) {
+    for (int64_t c = int64_t(tid) * 8; c < cols; c += 256 * 8) {
+      float v[8];
+      load8_t<DT>(x, base + c, v);
+#pragma unroll
+      for (int j = 0; j < 8; j++) take(v[j]);
+    }
+  } else {
+    for (int64_t c = tid; c < cols; c += 256) take(load_f(x, DT, base + c));
+  }
+  // merge (m, sum) over the wave, then over the four waves
+  for (int off = 32; off > 0; off >>= 1) {
+    const float om = __shfl_xor(m, off);
+    const float os = __shfl_xor(sum, off);
+    const float nm = fmaxf(m, om);
+    sum = (m == -INFINITY ? 0.f : sum * __expf(m - nm)) + (om == -INFINITY ? 0.f : os * __expf(om - nm));
+    m = nm;
+  }
+  __shared__ float red[2][4];
+  if ((tid & 63) == 0) {
+    red[0][tid >> 6] = m;
+    red[1][tid >> 6] = sum;
+  }
+  __syncthreads();
+  float M = red[0][0];
+  for (int w = 1; w < 4; w++) M = fmaxf(M, red[0][w]);
+  float S = 0.f;
+  for (int w = 0; w < 4; w++)
+    if (red[0][w] != -INFINITY) S += red[1][w] * __expf(red[0][w] - M);
+  const float inv = 1.0f / S;
+  if constexpr (VEC) {
+    for (int64_t c = int64_t(tid) * 8; c < cols; c += 256 * 8) {
+      float v[8];
+      load8_t<DT>(x, base + c, v);
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = __expf(v[j] * scale - M) * inv;
+      store8_t<DT>(y, base + c, v);
+    }
+  } else {
+    for (int64_t c = tid; c < cols; c += 256) store_f(y, DT, base + c, __expf(load_f(x, DT, base + c) * scale - M) * inv);
+  }
+}
+
+void launch_softmax(const void* x, void* y, int dtype, int64_t rows, int64_t cols, float scale, hipStream_t s) {
+  if (rows == 0 || cols == 0) return;
+  const bool vec = cols % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+#define NDX_SM(DT)                                                                                          \
+  do {                                                                                                      \
+    if (vec) hipLaunchKernelGGL((softmax_rows_kernel<DT, true>), dim3((unsigned)rows), dim3(256), 0, s, x, y, cols, scale); \
+    else hipLaunchKernelGGL((softmax_rows_kernel<DT, false>), dim3((unsigned)rows), dim3(256), 0, s, x, y, cols, scale);    \
+  } while (0)
+  if (dtype == NDX_BF16) NDX_SM(NDX_BF16);
+  else if (dtype == NDX_F16) NDX_SM(NDX_F16);
+  else NDX_SM(NDX_F32);
+#undef NDX_SM
+}
+
 }  // namespace ndx

@@ -229,6 +229,9 @@ int64_t attention_scratch_bytes(int B, int T, int S, int H, int d, int dv, int d
 void launch_head_norm_rotate(const HeadNormRotateArgs& a, hipStream_t s);
 void launch_row_norm(const RowNormArgs& a, hipStream_t s);
 void launch_group_norm(const GroupNormArgs& a, hipStream_t s);
+// Softmax of scale * x over the last axis of packed [rows, cols] rows, at
+// dtype (F32, BF16 or F16) in and out.
+void launch_softmax(const void* x, void* y, int dtype, int64_t rows, int64_t cols, float scale, hipStream_t s);
 void launch_conv2d(const ConvArgs& a, hipStream_t s);
 // The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, Cin]
 // (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types,

@@ -319,6 +319,12 @@ class Ops:
         return g._new("ndx_op_guided_euler_step", x.id, _id(uncond), cond.id, scalars.id)
 
     @staticmethod
+    def ActivationSoftmax(x, scale: float = 1.0):
+        """DmlOps.ActivationSoftmax over the last axis (Dml/DmlOps.cs:175-184)
+        of scale * x (scale: the alpha of the Gemm that made x)."""
+        return x.graph._new("ndx_op_softmax", x.id, float(scale))
+
+    @staticmethod
     def Patchify(x, patch, order=PATCH_CHANNEL_FIRST):
         return x.graph._new("ndx_op_patchify", x.id, int(patch), int(order))
 

@@ -70,7 +70,9 @@ class WeightSet:
             return self.cache[name]
         return self._register(name, self.weights[name], kind)
 
-    def stacked(self, names):
+    def stacked(self, names, kind: str = "weight"):
+        """The named tensors stacked along their first axis (matrices row
+        after row, vectors end to end), registered as kind."""
         key = "+".join(names)
         if key in self.cache:
             return self.cache[key]
@@ -81,7 +83,7 @@ class WeightSet:
         else:
             w = np.concatenate([np.asarray(x.Download().ToFloats() if isinstance(x, DeviceTensor) else x, np.float32)
                                 for x in ws], 0)
-        return self._register(key, w, "weight")
+        return self._register(key, w, kind)
 
     def columns(self, name, count):
         key = f"{name}[:, :{count}]"

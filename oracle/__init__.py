@@ -709,3 +709,51 @@ def lora_merge(weight, patches):
         up = _f32(np.asarray(up).reshape(-1, rank))
         lib().orc_lora_merge(flat, rows, cols, down, up, rank, float(np.float32(scale)), int(first), up.shape[0])
     return flat.reshape(w.shape)
+
+
+# ---- AutoencoderKL (Vae/AutoencoderKl.cs) ------------------------------------------
+
+def vae_resnet(x, w: dict, p: str, groups=32, eps=1e-6):
+    """AutoencoderKl.ResnetBlock (:16-35): GroupNorm-SiLU-conv twice, plus the
+    input (1x1-projected when the width changes)."""
+    x = _f32(x)
+    h = conv2d(group_norm(x, groups, w[f"{p}.norm1.weight"], w[f"{p}.norm1.bias"], eps, silu=True),
+               w[f"{p}.conv1.weight"], w[f"{p}.conv1.bias"], 1, 1)
+    h = conv2d(group_norm(h, groups, w[f"{p}.norm2.weight"], w[f"{p}.norm2.bias"], eps, silu=True),
+               w[f"{p}.conv2.weight"], w[f"{p}.conv2.bias"], 1, 1)
+    if f"{p}.conv_shortcut.weight" in w:
+        x = conv2d(x, w[f"{p}.conv_shortcut.weight"], w[f"{p}.conv_shortcut.bias"], 1, 0)
+    return x + h
+
+
+def vae_attention(x, w: dict, p: str, groups=32, eps=1e-6):
+    """AutoencoderKl.AttentionBlock (:40-63): single-head self-attention over
+    every pixel, softmax(q k^T / sqrt(C)) v, projected, plus the input."""
+    x = _f32(x)
+    n, c, h, wd = x.shape
+    t = group_norm(x, groups, w[f"{p}.group_norm.weight"], w[f"{p}.group_norm.bias"], eps)
+    t = np.ascontiguousarray(t.reshape(n, c, h * wd).transpose(0, 2, 1))
+    q = linear(t, w[f"{p}.to_q.weight"], w[f"{p}.to_q.bias"])
+    k = linear(t, w[f"{p}.to_k.weight"], w[f"{p}.to_k.bias"])
+    v = linear(t, w[f"{p}.to_v.weight"], w[f"{p}.to_v.bias"])
+    a = mha(q, k, v, 1, scale=float(np.float32(1.0) / np.sqrt(np.float32(c))))
+    o = linear(a, w[f"{p}.to_out.0.weight"], w[f"{p}.to_out.0.bias"])
+    return o.transpose(0, 2, 1).reshape(n, c, h, wd) + x
+
+
+def vae_decoder(latent, w: dict, block_out, layers_per_block=2, groups=32, eps=1e-6):
+    """AutoencoderKl.Decoder (:72-112) in fp32: latent [1, C, h, w] already
+    in the VAE's scale (LatentSpace.FromModelScale done) -> image [1, 3, H, W]."""
+    h = conv2d(latent, w["post_quant_conv.weight"], w["post_quant_conv.bias"], 1, 0)
+    h = conv2d(h, w["decoder.conv_in.weight"], w["decoder.conv_in.bias"], 1, 1)
+    h = vae_resnet(h, w, "decoder.mid_block.resnets.0", groups, eps)
+    h = vae_attention(h, w, "decoder.mid_block.attentions.0", groups, eps)
+    h = vae_resnet(h, w, "decoder.mid_block.resnets.1", groups, eps)
+    for i in range(len(block_out)):
+        p = f"decoder.up_blocks.{i}"
+        for j in range(layers_per_block + 1):
+            h = vae_resnet(h, w, f"{p}.resnets.{j}", groups, eps)
+        if f"{p}.upsamplers.0.conv.weight" in w:
+            h = conv2d(upsample_nearest(h), w[f"{p}.upsamplers.0.conv.weight"], w[f"{p}.upsamplers.0.conv.bias"], 1, 1)
+    h = group_norm(h, groups, w["decoder.conv_norm_out.weight"], w["decoder.conv_norm_out.bias"], eps, silu=True)
+    return conv2d(h, w["decoder.conv_out.weight"], w["decoder.conv_out.bias"], 1, 1)

@@ -553,3 +553,117 @@ def test_qwen_step_against_float64():
     c2, s2 = qwen.rope_tables(H, W, real, n_txt)
     assert np.max(np.abs(c2 - cos)) < 2e-6 and np.max(np.abs(s2 - sin)) < 2e-6
     assert np.array_equal(qwen.causal_table(real, n_txt), mask)
+
+
+# ---- AutoencoderKL's decoder (Vae/AutoencoderKl.cs) ------------------------------------------
+
+def vae_resnet64(x, w, p, groups, eps):
+    h = conv(group_norm(x, groups, w[f"{p}.norm1.weight"], w[f"{p}.norm1.bias"], eps, True),
+             w[f"{p}.conv1.weight"], w[f"{p}.conv1.bias"])
+    h = conv(group_norm(h, groups, w[f"{p}.norm2.weight"], w[f"{p}.norm2.bias"], eps, True),
+             w[f"{p}.conv2.weight"], w[f"{p}.conv2.bias"])
+    if f"{p}.conv_shortcut.weight" in w:
+        x = conv(x, w[f"{p}.conv_shortcut.weight"], w[f"{p}.conv_shortcut.bias"], 1, 0)
+    return np.asarray(x, f64) + h
+
+
+def vae_attention64(x, w, p, groups, eps):
+    x = np.asarray(x, f64)
+    B, C, H, W = x.shape
+    t = group_norm(x, groups, w[f"{p}.group_norm.weight"], w[f"{p}.group_norm.bias"], eps).reshape(B, C, -1)
+    t = t.transpose(0, 2, 1)
+    q, k, v = (lin(t, w[f"{p}.{n}.weight"], w[f"{p}.{n}.bias"]) for n in ("to_q", "to_k", "to_v"))
+    s = q @ k.transpose(0, 2, 1) / math.sqrt(C)
+    s = np.exp(s - s.max(-1, keepdims=True))
+    o = lin((s / s.sum(-1, keepdims=True)) @ v, w[f"{p}.to_out.0.weight"], w[f"{p}.to_out.0.bias"])
+    return o.transpose(0, 2, 1).reshape(B, C, H, W) + x
+
+
+def vae_decoder64(z, w, block_out, layers, groups, eps):
+    h = conv(conv(z, w["post_quant_conv.weight"], w["post_quant_conv.bias"], 1, 0),
+             w["decoder.conv_in.weight"], w["decoder.conv_in.bias"])
+    h = vae_resnet64(h, w, "decoder.mid_block.resnets.0", groups, eps)
+    h = vae_attention64(h, w, "decoder.mid_block.attentions.0", groups, eps)
+    h = vae_resnet64(h, w, "decoder.mid_block.resnets.1", groups, eps)
+    for i in range(len(block_out)):
+        for j in range(layers + 1):
+            h = vae_resnet64(h, w, f"decoder.up_blocks.{i}.resnets.{j}", groups, eps)
+        if f"decoder.up_blocks.{i}.upsamplers.0.conv.weight" in w:
+            h = conv(h.repeat(2, 2).repeat(2, 3), w[f"decoder.up_blocks.{i}.upsamplers.0.conv.weight"],
+                     w[f"decoder.up_blocks.{i}.upsamplers.0.conv.bias"])
+    h = group_norm(h, groups, w["decoder.conv_norm_out.weight"], w["decoder.conv_norm_out.bias"], eps, True)
+    return conv(h, w["decoder.conv_out.weight"], w["decoder.conv_out.bias"])
+
+
+def tiny_vae(seed):
+    from naivediffusion_amd import vae
+    cfg = vae.VaeConfig(block_out=(8, 16, 16), groups=4)
+    g = np.random.default_rng(seed)
+    w = {}
+    for name, shape in vae.decoder_weight_shapes(cfg).items():
+        if ".norm" in name or "group_norm" in name or "conv_norm_out" in name:
+            w[name] = (1.0 if name.endswith("weight") else 0.0) + rnd(g, *shape, s=0.1)
+        elif len(shape) == 1:
+            w[name] = rnd(g, *shape, s=0.1)
+        else:
+            w[name] = rnd(g, *shape, s=1.0 / math.sqrt(np.prod(shape[1:])))
+    return cfg, w, g
+
+
+def test_vae_decoder_shapes_follow_the_diffusers_layout():
+    """SDXL's VAE (block_out 128/256/512/512, 2 resnets a level, 3 in the
+    decoder): 14 resnets (2 mid + 4 x 3), one attention, three upsamplers,
+    the up blocks widest first, upsamplers on all but the last."""
+    from naivediffusion_amd import vae
+    shapes = vae.decoder_weight_shapes(vae.SDXL)
+    assert len([k for k in shapes if k.endswith(".conv1.weight")]) == 14
+    assert len([k for k in shapes if k.endswith("upsamplers.0.conv.weight")]) == 3
+    assert shapes["decoder.up_blocks.0.resnets.0.conv1.weight"] == (512, 512, 3, 3)
+    assert shapes["decoder.up_blocks.2.resnets.0.conv_shortcut.weight"] == (256, 512, 1, 1)
+    assert shapes["decoder.up_blocks.3.resnets.0.conv_shortcut.weight"] == (128, 256, 1, 1)
+    assert "decoder.up_blocks.3.upsamplers.0.conv.weight" not in shapes
+    assert shapes["decoder.conv_out.weight"] == (3, 128, 3, 3)
+
+
+@pytest.mark.parametrize("H,W", [(4, 4), (5, 3)])
+def test_vae_decoder_against_float64(H, W):
+    cfg, w, g = tiny_vae(11)
+    z = rnd(g, 1, 4, H, W, s=1.0)
+    got = oracle.vae_decoder(z, w, cfg.block_out, cfg.layers_per_block, cfg.groups, cfg.eps)
+    exp = vae_decoder64(z, w, cfg.block_out, cfg.layers_per_block, cfg.groups, cfg.eps)
+    assert got.shape == exp.shape == (1, 3, H * 4, W * 4)
+    assert close(got, exp, 5e-5)
+
+
+def test_vae_attention_pins():
+    """The attention block against float64; with a zero output projection
+    it is the identity; its scale is 1/sqrt(C) (1/sqrt of anything else, or
+    no softmax, gives another function)."""
+    cfg, w, g = tiny_vae(12)
+    p = "decoder.mid_block.attentions.0"
+    x = rnd(g, 1, 16, 3, 5, s=2.0)
+    got = oracle.vae_attention(x, w, p, cfg.groups, cfg.eps)
+    exp = vae_attention64(x, w, p, cfg.groups, cfg.eps)
+    assert close(got - x, exp - x)
+    w2 = dict(w)
+    w2[f"{p}.to_q.weight"] = w[f"{p}.to_q.weight"] * 4.0   # the same as a 4x larger scale
+    assert not close(oracle.vae_attention(x, w2, p, cfg.groups, cfg.eps) - x, exp - x, 1e-2)
+    w2 = dict(w, **{f"{p}.to_out.0.weight": np.zeros_like(w[f"{p}.to_out.0.weight"]),
+                    f"{p}.to_out.0.bias": np.zeros_like(w[f"{p}.to_out.0.bias"])})
+    assert np.array_equal(oracle.vae_attention(x, w2, p, cfg.groups, cfg.eps), x)
+
+
+def test_vae_resnet_with_zero_conv2_is_its_shortcut():
+    cfg, w, g = tiny_vae(13)
+    p = "decoder.up_blocks.1.resnets.1"   # 16 -> 16
+    w[f"{p}.conv2.weight"][:] = 0
+    w[f"{p}.conv2.bias"][:] = 0
+    x = rnd(g, 1, 16, 4, 6, s=1.0)
+    assert np.array_equal(oracle.vae_resnet(x, w, p, cfg.groups, cfg.eps), x)
+    p = "decoder.up_blocks.2.resnets.0"   # 16 -> 8 through a 1x1 shortcut keeping channels 5..12
+    for n in ("conv2.weight", "conv2.bias", "conv_shortcut.weight", "conv_shortcut.bias"):
+        w[f"{p}.{n}"][:] = 0
+    for o in range(8):
+        w[f"{p}.conv_shortcut.weight"][o, o + 5, 0, 0] = 1
+    x = rnd(g, 1, 16, 4, 6, s=1.0)
+    assert np.array_equal(oracle.vae_resnet(x, w, p, cfg.groups, cfg.eps), x[:, 5:13])
