@@ -412,14 +412,36 @@ def setup_vae(args, dev, seed, DT):
     )
 
 
+def setup_wan22(args, dev, seed, DT):
+    from naivediffusion_amd import rng, vae
+
+    cfg = vae.WAN22
+    compute = {"bf16": DT.BFloat16, "f32": DT.Float32, "f16": DT.Float16}[args.compute]
+    side = 1024
+    lat = side // cfg.scale_factor
+    weights = vae.wan22_device_weights(dev, cfg, seed, compute)
+    model = vae.build_wan22_decoder(dev, cfg, weights, side, side, compute)
+    inputs = [dev.Normal(DT.Float32, [1, cfg.latent_channels, lat, lat], rng.tensor_seed(seed, "latent"))]
+    out = [dev.Empty(compute, [1, 3, side, side])]
+    return dict(
+        model=model, inputs=inputs, out=out,
+        metric="Qwen-Image 2.1 VAE (Wan 2.2) decode s/image @1024x1024, 1 MI355X; % MFMA peak",
+        config={"workload": (f"Wan 2.2 VAE decoder on one frame (widths {'/'.join(map(str, cfg.widths))}), latent "
+                             f"{cfg.latent_channels}x{lat}x{lat} -> 3x{side}x{side}, {args.compute} compute"),
+                "batch": 1},
+        data="synthetic (seeded N(0,1) latent, N(0, 1/fan_in) weights made on the GPU)",
+        cpu=None,
+    )
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl", "qwen", "vae"], default="mmdit",
+    ap.add_argument("--workload", choices=["mmdit", "anima", "sdxl", "qwen", "vae", "wan22"], default="mmdit",
                     help="mmdit (the headline), or the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps, or the SDXL "
-                         "VAE decode")
+                         "(vae) / Qwen-Image 2.1 (wan22) VAE decodes")
     ap.add_argument("--compute", choices=["bf16", "f32", "f16"], default=None,
                     help="compute type (default bf16; fp16 for sdxl)")
     ap.add_argument("--int8", nargs="?", const="block32", default=None, choices=["block32", "channel"],
@@ -455,7 +477,7 @@ def main():
     log(f"device {dev.AdapterName}")
     t0 = time.perf_counter()
     setup = {"mmdit": setup_mmdit, "anima": setup_anima, "sdxl": setup_sdxl, "qwen": setup_qwen,
-             "vae": setup_vae}[args.workload](
+             "vae": setup_vae, "wan22": setup_wan22}[args.workload](
         args, dev, seed, DT)
     compiled = setup["model"].Compiled
     log(f"graph built and compiled in {time.perf_counter() - t0:.1f} s: {compiled.KernelCount} kernels/step, "

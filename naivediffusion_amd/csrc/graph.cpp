@@ -73,6 +73,8 @@ struct GNode {
   int64_t rows_split[5] = {0, 0, 0, 0, 0}, rows_off[5] = {0, 0, 0, 0, 0};
   // scratch in the arena, live only while this node runs
   int64_t scratch_bytes = 0, scratch_off = -1;
+  // a convolution on zero-padded channels: the input's own channel count
+  int64_t real_cin = 0;
   // the stream (0 the device's, 1 the second) the node runs on
   int lane = 0;
   // profiling
@@ -1092,7 +1094,9 @@ struct Compiler {
 
   // The filter value `wid` (a packed constant [Cout, Cin, kh, kw]) reordered
   // to [Cout, kh, kw, Cin] on the device, as a new constant value.
-  int reordered_filter(int wid) {
+  // With cin_pad above Cin the reordered filter has cin_pad channels, the
+  // extra ones zero (the convolution's NHWC input is padded to match).
+  int reordered_filter(int wid, int64_t cin_pad) {
     const GValue& w = values[wid];
     ndx_tensor* src = w.data;
     ndx_tensor* r;
@@ -1100,16 +1104,19 @@ struct Compiler {
     if (it != g->consts->nhwc_filters.end()) {
       r = it->second;
     } else {
-      r = new_tensor(g->dev, w.dtype, src->shape, src->rank);
+      const int64_t shape[4] = {w.v.size[0], cin_pad, w.v.size[2], w.v.size[3]};
+      r = new_tensor(g->dev, w.dtype, shape, 4);
       g->consts->tensors.push_back(r);
       g->consts->nhwc_filters[src] = r;
       launch_reorder_filter(src->ptr, r->ptr, w.dtype, w.v.size[0], w.v.size[1], w.v.size[2] * w.v.size[3],
-                            g->dev->stream);
+                            g->dev->stream, cin_pad);
       hip_check(hipGetLastError(), "filter reorder launch");
       hip_check(hipStreamSynchronize(g->dev->stream), "filter reorder");
     }
     GValue v = w;
     v.data = r;
+    v.v.size[1] = cin_pad;
+    v.v = packed4(v.v.size);
     values.push_back(v);
     int id = (int)values.size() - 1;
     values[id].base = id;
@@ -1185,7 +1192,7 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
     case OP_CONV: {
       const GValue& o = V[n.out];
       const GValue& x = V[n.in[0]];
-      n.flops = 2.0 * numel4(o.v) * x.v.size[1] * n.i3 * n.i4;
+      n.flops = 2.0 * numel4(o.v) * (n.real_cin ? n.real_cin : x.v.size[1]) * n.i3 * n.i4;
       n.bytes = bytes_of(n.in[0]) + bytes_of(n.in[1]) + out_b + bytes_of(n.in[2]) + bytes_of(n.in[3]);
       n.family = std::string("conv2d_") + dtype_name(x.dtype);
       if (n.i5) {
@@ -1520,17 +1527,20 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         const GValue& x = c.values[n.in[0]];
         const GValue& w = c.values[n.in[1]];
         const int64_t lim = int64_t(1) << 31;
-        const bool fits = x.v.size[1] * x.v.size[2] * x.v.size[3] * 2 < lim && numel4(w.v) * 2 < lim;
-        if (!w.quant && w.kind == VK_CONST && w.base == n.in[1] && w.offset == 0 && w.data && fits &&
-            conv_gemm_eligible(x.dtype, w.dtype, (int)x.v.size[1])) {
+        const int64_t cin = conv_gemm_cin(x.dtype, w.dtype, x.v.size[1]);
+        const bool fits = cin * x.v.size[2] * x.v.size[3] * 2 < lim && numel4(w.v) / x.v.size[1] * cin * 2 < lim;
+        if (!w.quant && w.kind == VK_CONST && w.base == n.in[1] && w.offset == 0 && w.data && cin && fits) {
           GNode t;
           t.op = OP_NHWC;
           t.lane = n.lane;
           t.in = {n.in[0]};
-          t.out = c.new_owner(x.dtype, x.v, 4);
+          View4 padded = x.v;
+          padded.size[1] = cin;
+          t.out = c.new_owner(x.dtype, padded, 4);
           sched.push_back(t);
+          n.real_cin = x.v.size[1];
           n.in[0] = t.out;
-          n.in[1] = c.reordered_filter(n.in[1]);
+          n.in[1] = c.reordered_filter(n.in[1], cin);
           n.i5 = 1;
         }
         break;
@@ -2042,7 +2052,9 @@ struct Runner {
         const GValue& x = val(n.in[0]);
         const int64_t c = n.i1 ? x.v.size[3] : x.v.size[1];
         const int64_t hw = n.i1 ? x.v.size[2] : x.v.size[2] * x.v.size[3];
-        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], c, hw, s);
+        // An NHWC copy for a convolution may have more (zero) channels than x.
+        const int64_t c_pad = n.i1 ? c : val(n.out).v.size[1];
+        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], c, hw, s, c_pad);
         break;
       }
       case OP_UPSAMPLE: {

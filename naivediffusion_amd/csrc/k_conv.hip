@@ -103,8 +103,36 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_vec_kernel(const uint16_t* x
   }
 }
 
-void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s) {
+// The same transposition into pixel rows of c_pad > c channels, the
+// channels past c written as zeros (the implicit-GEMM convolution reads its
+// K in 64-channel tiles).
+__global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* x, uint16_t* y, int64_t c,
+                                                               int64_t c_pad, int64_t hw) {
+  __shared__ uint16_t tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t c0 = int64_t(blockIdx.y) * 64, p0 = int64_t(blockIdx.x) * 64;
+  const uint16_t* xb = x + b * c * hw;
+  uint16_t* yb = y + b * c_pad * hw;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t ch = c0 + r, p = p0 + tx;
+    tile[r][tx] = (ch < c && p < hw) ? xb[ch * hw + p] : uint16_t(0);
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t p = p0 + r, ch = c0 + tx;
+    if (ch < c_pad && p < hw) yb[p * c_pad + ch] = tile[tx][r];
+  }
+}
+
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s,
+                         int64_t c_pad) {
   if (dtype_size(dtype) != 2) throw std::runtime_error("nchw_to_nhwc: 16-bit elements only");
+  if (c_pad > c) {
+    dim3 g((unsigned)((hw + 63) / 64), (unsigned)((c_pad + 63) / 64), (unsigned)n);
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, c_pad, hw);
+    return;
+  }
   dim3 g((unsigned)((hw + 63) / 64), (unsigned)((c + 63) / 64), (unsigned)n);
   if (c % 64 == 0 && hw % 64 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0) {
     hipLaunchKernelGGL(nchw_to_nhwc_vec_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, hw);
@@ -113,22 +141,25 @@ void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c
   hipLaunchKernelGGL(nchw_to_nhwc_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, hw);
 }
 
-// Filters [cout, cin, taps] -> [cout, taps, cin] (16-bit elements).
-__global__ void reorder_filter_kernel(const uint16_t* w, uint16_t* y, int64_t cout, int64_t cin, int64_t taps) {
-  const int64_t total = cout * cin * taps;
+// Filters [cout, cin, taps] -> [cout, taps, cin_pad] (16-bit elements),
+// channels past cin zero.
+__global__ void reorder_filter_kernel(const uint16_t* w, uint16_t* y, int64_t cout, int64_t cin, int64_t taps,
+                                      int64_t cin_pad) {
+  const int64_t total = cout * cin_pad * taps;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t ci = i % cin, t = (i / cin) % taps, co = i / (cin * taps);
-    y[i] = w[(co * cin + ci) * taps + t];
+    const int64_t ci = i % cin_pad, t = (i / cin_pad) % taps, co = i / (cin_pad * taps);
+    y[i] = ci < cin ? w[(co * cin + ci) * taps + t] : uint16_t(0);
   }
 }
 
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
-                           hipStream_t s) {
+                           hipStream_t s, int64_t cin_pad) {
   if (dtype_size(dtype) != 2) throw std::runtime_error("reorder_filter: 16-bit elements only");
-  const int64_t total = cout * cin * taps;
+  if (cin_pad < cin) cin_pad = cin;
+  const int64_t total = cout * cin_pad * taps;
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(reorder_filter_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, s, (const uint16_t*)w,
-                     (uint16_t*)y, cout, cin, taps);
+                     (uint16_t*)y, cout, cin, taps, cin_pad);
 }
 
 void launch_conv2d(const ConvArgs& a, hipStream_t s) {

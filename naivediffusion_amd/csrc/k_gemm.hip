@@ -1454,8 +1454,11 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
 // [Cout, kh, kw, Cin] and X_b the implicit im2col of the NHWC input: the
 // output lands in NCHW directly (rows are channels, columns pixels).
 
-bool conv_gemm_eligible(int x_dtype, int w_dtype, int cin) {
-  return (x_dtype == NDX_BF16 || x_dtype == NDX_F16) && w_dtype == x_dtype && cin % BK == 0;
+int64_t conv_gemm_cin(int x_dtype, int w_dtype, int64_t cin) {
+  if (!((x_dtype == NDX_BF16 || x_dtype == NDX_F16) && w_dtype == x_dtype)) return 0;
+  if (cin % BK == 0) return cin;
+  const int64_t pad = (cin + BK - 1) / BK * BK;
+  return cin % 8 == 0 && 2 * pad <= 3 * cin ? pad : 0;
 }
 
 enum ConvKind { CK_256, CK_128, CK_64x128, CK_64x64 };

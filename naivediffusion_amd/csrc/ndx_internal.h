@@ -235,12 +235,16 @@ void launch_softmax(const void* x, void* y, int dtype, int64_t rows, int64_t col
 void launch_conv2d(const ConvArgs& a, hipStream_t s);
 // The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, Cin]
 // (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types,
-// Cin a multiple of 64.
-bool conv_gemm_eligible(int x_dtype, int w_dtype, int cin);
+// Cin a multiple of 64. conv_gemm_cin is the channel count the GEMM runs
+// with: Cin itself, Cin rounded up to a multiple of 64 (the NHWC copy and the
+// filter padded with zero channels) where that adds at most half, or 0 when
+// the direct kernel should run instead.
+int64_t conv_gemm_cin(int x_dtype, int w_dtype, int64_t cin);
 void launch_conv_gemm(const ConvArgs& a, hipStream_t s);
-void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s);
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s,
+                         int64_t c_pad = 0);
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
-                           hipStream_t s);
+                           hipStream_t s, int64_t cin_pad = 0);
 const char* conv_family(const ConvArgs& a);
 void launch_elementwise(const ElemArgs& a, hipStream_t s);
 void launch_upsample(const UpsampleArgs& a, hipStream_t s);

@@ -757,3 +757,81 @@ def vae_decoder(latent, w: dict, block_out, layers_per_block=2, groups=32, eps=1
             h = conv2d(upsample_nearest(h), w[f"{p}.upsamplers.0.conv.weight"], w[f"{p}.upsamplers.0.conv.bias"], 1, 1)
     h = group_norm(h, groups, w["decoder.conv_norm_out.weight"], w["decoder.conv_norm_out.bias"], eps, silu=True)
     return conv2d(h, w["decoder.conv_out.weight"], w["decoder.conv_out.bias"], 1, 1)
+
+
+# ---- Wan 2.2's VAE on one frame (Vae/Wan22Vae.cs, Vae/WanVae.cs) ------------------------------
+
+def wan_channel_rms(x, gamma):
+    """WanVae.ChannelRmsNorm (:103-113): per pixel, x / sqrt(mean over the
+    channels of x^2 + 1e-24 / C) * gamma. x [1, C, H, W]."""
+    x = _f32(x)
+    n, c, h, w = x.shape
+    t = np.ascontiguousarray(x.reshape(c, h * w).T)
+    y = rms_norm(t, gamma, float(np.float32(1e-24 / c)))
+    return np.ascontiguousarray(y.T.reshape(n, c, h, w))
+
+
+def wan_residual(x, w: dict, p: str):
+    """WanVae.ResidualBlock (:121-132)."""
+    x = _f32(x)
+    h = conv2d(silu(wan_channel_rms(x, w[f"{p}.residual.0.gamma"])), w[f"{p}.residual.2.weight"],
+               w[f"{p}.residual.2.bias"], 1, 1)
+    h = conv2d(silu(wan_channel_rms(h, w[f"{p}.residual.3.gamma"])), w[f"{p}.residual.6.weight"],
+               w[f"{p}.residual.6.bias"], 1, 1)
+    if f"{p}.shortcut.weight" in w:
+        x = conv2d(x, w[f"{p}.shortcut.weight"], w[f"{p}.shortcut.bias"], 1, 0)
+    return x + h
+
+
+def wan_attention(x, w: dict, p: str):
+    """WanVae.AttentionBlock (:134-151): one head of C features over every
+    pixel; the 1x1 projections as products over the pixels' rows."""
+    x = _f32(x)
+    n, c, h, wd = x.shape
+    t = np.ascontiguousarray(wan_channel_rms(x, w[f"{p}.norm.gamma"]).reshape(c, h * wd).T)
+    qkv = linear(t, np.asarray(w[f"{p}.to_qkv.weight"]).reshape(3 * c, c), w[f"{p}.to_qkv.bias"])
+    q, k, v = (np.ascontiguousarray(qkv[:, i * c:(i + 1) * c]) for i in range(3))
+    a = mha(q, k, v, 1, scale=float(np.float32(1.0) / np.sqrt(np.float32(c))))
+    o = linear(a, np.asarray(w[f"{p}.proj.weight"]).reshape(c, c), w[f"{p}.proj.bias"])
+    return np.ascontiguousarray(o.reshape(h * wd, c).T.reshape(n, c, h, wd)) + x
+
+
+def wan_up_shortcut(x, out_channels, temporal):
+    """Wan22Vae.UpShortcut (:153-189) by indexing: the same width is a
+    nearest upsample; half the width is the odd channels upsampled (a level
+    that doubled time), else out[o, 2y + r, 2x + s] = x[2o + r, y, x]."""
+    x = _f32(x)
+    n, c, h, w = x.shape
+    if c == out_channels:
+        return upsample_nearest(x)
+    if temporal:
+        return upsample_nearest(np.ascontiguousarray(x[:, 1::2]))
+    out = np.empty((n, out_channels, 2 * h, 2 * w), np.float32)
+    for r in range(2):
+        out[:, :, r::2, :] = np.repeat(x[:, r::2], 2, axis=3)
+    return out
+
+
+def wan22_decoder(z, w: dict, temporal=(False, True, True, True)):
+    """Wan22Vae.Decoder (:191-238) in fp32: z [1, 64, h, w] already on the
+    VAE's scale -> RGB [1, 3, 16h, 16w]."""
+    h = conv2d(z, w["conv2.weight"], w["conv2.bias"], 1, 0)
+    h = conv2d(h, w["decoder.conv1.weight"], w["decoder.conv1.bias"], 1, 1)
+    h = wan_residual(h, w, "decoder.middle.0")
+    h = wan_attention(h, w, "decoder.middle.1")
+    h = wan_residual(h, w, "decoder.middle.2")
+    levels = 0
+    while f"decoder.upsamples.{levels}.upsamples.0.residual.0.gamma" in w:
+        levels += 1
+    for level in range(levels):
+        p = f"decoder.upsamples.{level}.upsamples"
+        level_in = h
+        i = 0
+        while f"{p}.{i}.residual.0.gamma" in w:
+            h = wan_residual(h, w, f"{p}.{i}")
+            i += 1
+        if level != levels - 1:
+            h = conv2d(upsample_nearest(h), w[f"{p}.{i}.resample.1.weight"], w[f"{p}.{i}.resample.1.bias"], 1, 1)
+            h = h + wan_up_shortcut(level_in, h.shape[1], temporal[levels - 2 - level])
+    h = silu(wan_channel_rms(h, w["decoder.head.0.gamma"]))
+    return conv2d(h, w["decoder.head.2.weight"], w["decoder.head.2.bias"], 1, 1)[:, :3]

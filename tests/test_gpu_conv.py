@@ -57,6 +57,12 @@ CASES = [
     (1, 128, 16, 16, 64, 1, 1, 0),
     (2, 640, 8, 8, 1280, 3, 1, 1),
     (1, 192, 9, 31, 96, 3, 1, 1),
+    # Channel counts that are multiples of 8 but not of 64 (the Wan VAE's
+    # 144 and 288): the NHWC copy and the filter padded with zero channels
+    # to 192 and 320.
+    (1, 144, 13, 11, 144, 3, 1, 1),
+    (2, 288, 7, 9, 144, 1, 1, 0),
+    (1, 288, 10, 6, 576, 3, 2, 1),
 ]
 
 

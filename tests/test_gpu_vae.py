@@ -1,4 +1,5 @@
-"""GPU parity of the VAE decoder (AutoencoderKl.Decoder, Vae/AutoencoderKl.cs)
+"""GPU parity of the VAE decoders (AutoencoderKl.Decoder, Vae/AutoencoderKl.cs;
+Wan22Vae.Decoder, Vae/Wan22Vae.cs)
 against the oracle's composition, which a float64 restatement pins: a small
 decoder of the same layout at fp32 (1e-3) and bf16 (2e-2), SDXL's own widths
 on a 16x16 latent (a 128x128 image), and the full 1024x1024 decode checked
@@ -106,6 +107,75 @@ def test_full_size_decode_properties(device):
     for compute in (DT.BFloat16, DT.Float32):
         say(f"vae decoder 1024x1024 {compute.name}")
         dec = vae.AutoencoderKlDecoder(device, cfg, weights, 1024, 1024, compute)
+        out[compute] = dec.Decode(latent)
+        dec.Dispose()
+        assert out[compute].shape == (1, 3, 1024, 1024)
+        assert np.isfinite(out[compute]).all()
+    err = rel_err(out[DT.BFloat16], out[DT.Float32])
+    say(f"  bf16 vs fp32 {err:.2e}")
+    assert err <= 5e-2
+
+
+# ---- Wan 2.2's single-frame decoder (Qwen-Image 2.1's VAE) ---------------------------------
+
+def wan_case(cfg, seed, h, w, weight_dtype=DT.BFloat16):
+    weights = vae.wan22_synthetic_weights(cfg, seed, weight_dtype)
+    latent = rng.normal(rng.tensor_seed(seed, "latent"), (1, cfg.latent_channels, h, w))
+    return weights, latent.astype(np.float32)
+
+
+def wan_oracle(cfg, weights, latent):
+    """FromModelScale in float32 (latent * deviation + mean, each rounded),
+    then the oracle's decoder."""
+    lc = cfg.latent_channels
+    dev = np.asarray(vae.WAN22_DEVIATIONS[:lc], np.float32)[None, :, None, None]
+    mean = np.asarray(vae.WAN22_MEANS[:lc], np.float32)[None, :, None, None]
+    z = (latent * dev).astype(np.float32) + mean
+    return oracle.wan22_decoder(z.astype(np.float32), weights, vae.WAN22_TEMPORAL)
+
+
+WAN_SMALL = vae.Wan22Config(latent_channels=16, widths=(128, 128, 64, 32, 32), resnets=3)
+
+
+@pytest.mark.parametrize("compute,tol", [(DT.Float32, 1e-3), (DT.BFloat16, 2e-2)])
+def test_wan22_small_decoder_against_oracle(device, compute, tol):
+    """Every level kind: same-width shortcuts, the odd channels of a level
+    that doubled time, the row interleave of one that did not."""
+    cfg = WAN_SMALL
+    weights, latent = wan_case(cfg, 31, 3, 5)
+    say(f"wan 2.2 decoder (128..32) 3x5 latent {compute.name}")
+    dec = vae.Wan22Decoder(device, cfg, weights, 48, 80, compute)
+    got = dec.Decode(latent)
+    dec.Dispose()
+    want = wan_oracle(cfg, weights, latent)
+    err = rel_err(got.reshape(want.shape), want)
+    say(f"  rel err {err:.2e}")
+    assert got.shape == (1, 3, 48, 80) and err <= tol
+
+
+@pytest.mark.parametrize("compute,tol", [(DT.BFloat16, 2e-2), (DT.Float32, 1e-3)])
+def test_wan22_real_widths_on_a_small_latent(device, compute, tol):
+    cfg = vae.WAN22
+    weights, latent = wan_case(cfg, 32, 2, 3)
+    say(f"wan 2.2 decoder at 1152..144 wide, 2x3 latent, {compute.name}")
+    dec = vae.Wan22Decoder(device, cfg, weights, 32, 48, compute)
+    got = dec.Decode(latent)
+    dec.Dispose()
+    say("  oracle")
+    want = wan_oracle(cfg, weights, latent)
+    err = rel_err(got.reshape(want.shape), want)
+    say(f"  rel err {err:.2e}")
+    assert got.shape == (1, 3, 32, 48) and err <= tol
+
+
+def test_wan22_full_size_decode_properties(device):
+    """1024x1024 from a 64x64 latent: finite, bf16 within 5e-2 of fp32."""
+    cfg = vae.WAN22
+    weights, latent = wan_case(cfg, 33, 64, 64)
+    out = {}
+    for compute in (DT.BFloat16, DT.Float32):
+        say(f"wan 2.2 decoder 1024x1024 {compute.name}")
+        dec = vae.Wan22Decoder(device, cfg, weights, 1024, 1024, compute)
         out[compute] = dec.Decode(latent)
         dec.Dispose()
         assert out[compute].shape == (1, 3, 1024, 1024)

@@ -667,3 +667,118 @@ def test_vae_resnet_with_zero_conv2_is_its_shortcut():
         w[f"{p}.conv_shortcut.weight"][o, o + 5, 0, 0] = 1
     x = rnd(g, 1, 16, 4, 6, s=1.0)
     assert np.array_equal(oracle.vae_resnet(x, w, p, cfg.groups, cfg.eps), x[:, 5:13])
+
+
+# ---- Wan 2.2's single-frame decoder (Vae/Wan22Vae.cs, Vae/WanVae.cs) ------------------------
+
+def channel_rms64(x, g):
+    x = np.asarray(x, f64)
+    c = x.shape[1]
+    return x / np.sqrt((x * x).mean(1, keepdims=True) + 1e-24 / c) * np.asarray(g, f64)[None, :, None, None]
+
+
+def wan_residual64(x, w, p):
+    h = conv(silu(channel_rms64(x, w[f"{p}.residual.0.gamma"])), w[f"{p}.residual.2.weight"], w[f"{p}.residual.2.bias"])
+    h = conv(silu(channel_rms64(h, w[f"{p}.residual.3.gamma"])), w[f"{p}.residual.6.weight"], w[f"{p}.residual.6.bias"])
+    if f"{p}.shortcut.weight" in w:
+        x = conv(x, w[f"{p}.shortcut.weight"], w[f"{p}.shortcut.bias"], 1, 0)
+    return np.asarray(x, f64) + h
+
+
+def wan_attention64(x, w, p):
+    x = np.asarray(x, f64)
+    _, c, H, W = x.shape
+    qkv = conv(channel_rms64(x, w[f"{p}.norm.gamma"]), w[f"{p}.to_qkv.weight"], w[f"{p}.to_qkv.bias"], 1, 0)
+    q, k, v = (qkv[0, i * c:(i + 1) * c].reshape(c, -1).T for i in range(3))
+    s = q @ k.T / math.sqrt(c)
+    s = np.exp(s - s.max(-1, keepdims=True))
+    a = (s / s.sum(-1, keepdims=True)) @ v
+    o = conv(a.T.reshape(1, c, H, W), w[f"{p}.proj.weight"], w[f"{p}.proj.bias"], 1, 0)
+    return o + x
+
+
+def tiny_wan(seed, widths=(16, 16, 8, 4, 4)):
+    from naivediffusion_amd import vae
+    cfg = vae.Wan22Config(latent_channels=8, widths=widths, resnets=2)
+    g = np.random.default_rng(seed)
+    w = {}
+    for name, shape in vae.wan22_decoder_shapes(cfg).items():
+        if name.endswith(".gamma"):
+            w[name] = 1.0 + rnd(g, *shape, s=0.1)
+        elif len(shape) == 1:
+            w[name] = rnd(g, *shape, s=0.1)
+        else:
+            w[name] = rnd(g, *shape, s=1.0 / math.sqrt(np.prod(shape[1:])))
+    return cfg, w, g
+
+
+def test_wan_up_shortcut_moves_each_value_where_dup_up_puts_it():
+    """DupUp3D on one frame, checked element by element: the same width a
+    nearest upsample; half the width either the odd channels upsampled or
+    out[o, 2y + r, 2x + s] = x[2o + r, y, x]."""
+    g = np.random.default_rng(1)
+    x = rnd(g, 1, 8, 3, 5, s=1.0)
+    same = oracle.wan_up_shortcut(x, 8, False)
+    assert np.array_equal(same, x.repeat(2, 2).repeat(2, 3))
+    odd = oracle.wan_up_shortcut(x, 4, True)
+    assert np.array_equal(odd, x[:, [1, 3, 5, 7]].repeat(2, 2).repeat(2, 3))
+    inter = oracle.wan_up_shortcut(x, 4, False)
+    for o in range(4):
+        for yy in range(6):
+            for xx in range(10):
+                assert inter[0, o, yy, xx] == x[0, 2 * o + yy % 2, yy // 2, xx // 2]
+
+
+def test_wan_blocks_against_float64():
+    cfg, w, g = tiny_wan(2)
+    x = rnd(g, 1, 16, 4, 5, s=1.0)
+    assert close(oracle.wan_residual(x, w, "decoder.middle.0"), wan_residual64(x, w, "decoder.middle.0"))
+    p = "decoder.upsamples.2.upsamples.0"   # 16 -> 8 through the 1x1 shortcut
+    assert close(oracle.wan_residual(x, w, p), wan_residual64(x, w, p))
+    got = oracle.wan_attention(x, w, "decoder.middle.1")
+    exp = wan_attention64(x, w, "decoder.middle.1")
+    assert close(got - x, exp - x)
+    # the norm is over channels, per pixel: scaling one pixel's channels leaves its normalised values
+    y = x.copy()
+    y[:, :, 1, 2] *= 7.0
+    a = oracle.wan_channel_rms(x, w["decoder.middle.0.residual.0.gamma"])
+    b = oracle.wan_channel_rms(y, w["decoder.middle.0.residual.0.gamma"])
+    assert np.allclose(a, b, rtol=1e-5, atol=1e-6)
+    # zero second convolution: the block is its shortcut
+    w[f"{p}.residual.6.weight"][:] = 0
+    w[f"{p}.residual.6.bias"][:] = 0
+    sc = oracle.conv2d(x, w[f"{p}.shortcut.weight"], w[f"{p}.shortcut.bias"], 1, 0)
+    assert np.array_equal(oracle.wan_residual(x, w, p), sc)
+
+
+def test_wan22_decoder_against_float64():
+    cfg, w, g = tiny_wan(3)
+    z = rnd(g, 1, 8, 2, 3, s=1.0)
+    got = oracle.wan22_decoder(z, w)
+    h = conv(conv(z, w["conv2.weight"], w["conv2.bias"], 1, 0), w["decoder.conv1.weight"], w["decoder.conv1.bias"])
+    h = wan_residual64(h, w, "decoder.middle.0")
+    h = wan_attention64(h, w, "decoder.middle.1")
+    h = wan_residual64(h, w, "decoder.middle.2")
+    flags = (True, True, True, False)   # levels 0..3 from the latent: entries 3, 2, 1, 0 of (F, T, T, T)
+    for level in range(5):
+        p = f"decoder.upsamples.{level}.upsamples"
+        inp = h
+        for i in range(cfg.resnets):
+            h = wan_residual64(h, w, f"{p}.{i}")
+        if level < 4:
+            h = conv(h.repeat(2, 2).repeat(2, 3), w[f"{p}.{cfg.resnets}.resample.1.weight"],
+                     w[f"{p}.{cfg.resnets}.resample.1.bias"])
+            c_in, c_out = inp.shape[1], h.shape[1]
+            if c_in == c_out:
+                sc = inp.repeat(2, 2).repeat(2, 3)
+            elif flags[level]:
+                sc = inp[:, 1::2].repeat(2, 2).repeat(2, 3)
+            else:
+                sc = np.empty_like(h)
+                for r in range(2):
+                    sc[:, :, r::2, :] = inp[:, r::2].repeat(2, 3)
+            h = h + sc
+    h = conv(silu(channel_rms64(h, w["decoder.head.0.gamma"])), w["decoder.head.2.weight"], w["decoder.head.2.bias"])
+    exp = h[:, :3]
+    assert got.shape == exp.shape == (1, 3, 32, 48)
+    assert close(got, exp, 5e-5)
