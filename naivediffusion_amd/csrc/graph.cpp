@@ -73,8 +73,11 @@ struct GNode {
   int64_t rows_split[5] = {0, 0, 0, 0, 0}, rows_off[5] = {0, 0, 0, 0, 0};
   // scratch in the arena, live only while this node runs
   int64_t scratch_bytes = 0, scratch_off = -1;
-  // a convolution on zero-padded channels: the input's own channel count
-  int64_t real_cin = 0;
+  // An implicit-GEMM convolution: the reordered filter's channels per tap
+  // (a multiple of 64, zeros past the input's own), and whether the input is
+  // read through a nearest 2x upsample (a fused UpsampleNearest).
+  int64_t conv_cin_k = 0;
+  int conv_up = 0;
   // the stream (0 the device's, 1 the second) the node runs on
   int lane = 0;
   // profiling
@@ -1093,9 +1096,8 @@ struct Compiler {
   }
 
   // The filter value `wid` (a packed constant [Cout, Cin, kh, kw]) reordered
-  // to [Cout, kh, kw, Cin] on the device, as a new constant value.
-  // With cin_pad above Cin the reordered filter has cin_pad channels, the
-  // extra ones zero (the convolution's NHWC input is padded to match).
+  // to [Cout, kh, kw, cin_pad] on the device, as a new constant value, the
+  // channels past Cin zero.
   int reordered_filter(int wid, int64_t cin_pad) {
     const GValue& w = values[wid];
     ndx_tensor* src = w.data;
@@ -1192,20 +1194,22 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
     case OP_CONV: {
       const GValue& o = V[n.out];
       const GValue& x = V[n.in[0]];
-      n.flops = 2.0 * numel4(o.v) * (n.real_cin ? n.real_cin : x.v.size[1]) * n.i3 * n.i4;
+      n.flops = 2.0 * numel4(o.v) * x.v.size[1] * n.i3 * n.i4;
       n.bytes = bytes_of(n.in[0]) + bytes_of(n.in[1]) + out_b + bytes_of(n.in[2]) + bytes_of(n.in[3]);
       n.family = std::string("conv2d_") + dtype_name(x.dtype);
       if (n.i5) {
         ConvArgs a{};
         a.N = (int)x.v.size[0];
         a.Cin = (int)x.v.size[1];
-        a.H = (int)x.v.size[2];
-        a.W = (int)x.v.size[3];
+        a.H = (int)x.v.size[2] << n.conv_up;
+        a.W = (int)x.v.size[3] << n.conv_up;
         a.Cout = (int)o.v.size[1];
         a.kh = n.i3;
         a.kw = n.i4;
         a.Ho = (int)o.v.size[2];
         a.Wo = (int)o.v.size[3];
+        a.cin_k = (int)n.conv_cin_k;
+        a.up = n.conv_up;
         n.family = conv_family(a);
       }
       break;
@@ -1223,7 +1227,9 @@ void prof_info(GNode& n, const std::vector<GValue>& V) {
                                     "softmax"};
       static_assert(sizeof(names) / sizeof(names[0]) == OP_SOFTMAX + 1, "a kernel family name per operator");
       n.family = names[n.op];
-      if (n.op == OP_ROWNORM) n.family = n.i0 == 0 ? "layer_norm" : n.i0 == 1 ? "modulate" : "rms_norm";
+      if (n.op == OP_ROWNORM)
+        n.family = n.i1 ? (n.i0 == 0 ? "channel_layer_norm" : "channel_rms_norm")
+                        : (n.i0 == 0 ? "layer_norm" : n.i0 == 1 ? "modulate" : "rms_norm");
     }
   }
 }
@@ -1425,6 +1431,73 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     n.in[1] = p.in[0];
   }
 
+  // The K channels per tap an implicit-GEMM convolution of `n` runs with
+  // over input value xid (read through a 2x upsample when up), or 0 when
+  // the direct kernel runs: 16-bit filters held as constants, and 32-bit
+  // offsets into the input image and the filter.
+  auto conv_gemm_k = [&](const GNode& n, int xid) -> int64_t {
+    const GValue& x = c.values[xid];
+    const GValue& w = c.values[n.in[1]];
+    if (w.quant || w.kind != VK_CONST || w.base != n.in[1] || w.offset != 0 || !w.data) return 0;
+    const int64_t cin = conv_gemm_cin(x.dtype, w.dtype, x.v.size[1]);
+    const int64_t lim = int64_t(1) << 31;
+    if (!cin || x.v.size[1] * x.v.size[2] * x.v.size[3] * 2 >= lim || numel4(w.v) / x.v.size[1] * cin * 2 >= lim)
+      return 0;
+    return cin;
+  };
+
+  // Rewrite: a nearest 2x upsample read only by an implicit-GEMM
+  // convolution (UpsampleNearest then a 3x3 convolution: the decoders'
+  // upsamplers) is never materialised; the convolution reads each
+  // upsampled pixel from its source.
+  for (auto& n : src) {
+    if (n.op != OP_CONV) continue;
+    const int uid = n.in[0];
+    const GValue& uv = c.values[uid];
+    if (uv.kind != VK_NODE || uv.base != uid || uv.producer < 0 || uses[uid] != 1) continue;
+    if (std::find(outs.begin(), outs.end(), uid) != outs.end()) continue;
+    const GNode& p = src[uv.producer];
+    if (p.op != OP_UPSAMPLE || p.i0 != 2 || p.lane != n.lane || !conv_gemm_k(n, p.in[0])) continue;
+    n.in[0] = p.in[0];
+    n.conv_up = 1;
+  }
+
+  // Rewrite: the LayerNorm or RMSNorm of an image's token view [N, 1, P, C]
+  // (a packed [N, C, P] seen as tokens; the Wan VAE's channel norms,
+  // Vae/WanVae.cs:103-113) reads the image as it lies and writes the tokens
+  // (i1 = 1), with no transposed copy first; a SiLU that alone reads such a
+  // norm's output joins it (i2 = 1).
+  auto one_row = [&](int id) {
+    if (id < 0) return true;
+    const View4& v = c.values[id].v;
+    return !c.values[c.values[id].base].quant && v.size[0] == 1 && v.size[1] == 1 && v.size[2] == 1 &&
+           (v.size[3] == 1 || v.stride[3] == 1);
+  };
+  for (auto& n : src) {
+    if (n.op != OP_ROWNORM || n.i0 == 1 || n.rows_split[1] || n.rows_split[2]) continue;
+    const GValue& x = c.values[n.in[0]];
+    const View4& v = x.v;
+    if (c.values[x.base].quant || x.offset != 0 || v.size[1] != 1 || v.size[2] < 2 || v.size[3] < 2 ||
+        v.stride[2] != 1 || v.stride[3] != v.size[2] || (v.size[0] > 1 && v.stride[0] != v.size[2] * v.size[3]))
+      continue;
+    if (!one_row(n.in[1]) || !one_row(n.in[2])) continue;
+    n.i1 = 1;
+  }
+  for (auto& n : src) {
+    if (n.op != OP_ELEM || n.i0 != ELEM_SILU || n.in.empty() || n.in[0] < 0 || (n.in.size() > 1 && n.in[1] >= 0))
+      continue;
+    const int nid = n.in[0];
+    const GValue& nv = c.values[nid];
+    if (nv.kind != VK_NODE || nv.base != nid || nv.producer < 0 || uses[nid] != 1) continue;
+    if (std::find(outs.begin(), outs.end(), nid) != outs.end()) continue;
+    const GNode& p = src[nv.producer];
+    if (p.op != OP_ROWNORM || !p.i1 || p.i2 || p.lane != n.lane || nv.dtype != c.values[n.out].dtype) continue;
+    GNode fused = p;
+    fused.out = n.out;
+    fused.i2 = 1;
+    n = fused;
+  }
+
   // Reachability from the outputs (through views to their owners).
   std::vector<char> need_node(src.size(), 0);
   std::function<void(int)> mark_value = [&](int id) {
@@ -1496,6 +1569,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         ensure_packed(n.in[3]);
         break;
       case OP_ROWNORM:
+        if (n.i1) break;  // a channel norm: the image and one-row parameters as they are
         ensure_rows(n.in[0]);
         for (int j = 1; j < 3; j++) {
           if (n.in[j] < 0) continue;
@@ -1519,30 +1593,36 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
         break;
       case OP_CONV: {
-        for (auto& id : n.in)
-          if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
-        // 16-bit filters over a multiple of 64 input channels run as an
-        // implicit GEMM: the input copied to NHWC just before, the filter
+        for (size_t j = 1; j < n.in.size(); j++)
+          if (n.in[j] >= 0 && !c.values[c.values[n.in[j]].base].quant) ensure_packed(n.in[j]);
+        const int64_t cin_k = conv_gemm_k(n, n.in[0]);
+        if (!cin_k) {
+          if (n.conv_up) fail(NDX_UNSUPPORTED, "a fused upsample needs the implicit-GEMM convolution");
+          ensure_packed(n.in[0]);
+          break;
+        }
+        // The implicit GEMM reads its input in NHWC: an image whose view
+        // already lies that way (a norm's token rows seen as an image) in
+        // place, any other copied to NHWC just before. The filter is
         // reordered once.
         const GValue& x = c.values[n.in[0]];
-        const GValue& w = c.values[n.in[1]];
-        const int64_t lim = int64_t(1) << 31;
-        const int64_t cin = conv_gemm_cin(x.dtype, w.dtype, x.v.size[1]);
-        const bool fits = cin * x.v.size[2] * x.v.size[3] * 2 < lim && numel4(w.v) / x.v.size[1] * cin * 2 < lim;
-        if (!w.quant && w.kind == VK_CONST && w.base == n.in[1] && w.offset == 0 && w.data && cin && fits) {
+        const View4& v = x.v;
+        const bool nhwc = x.offset % 8 == 0 && v.stride[1] == 1 && v.stride[3] == v.size[1] &&
+                          v.stride[2] == v.size[3] * v.size[1] &&
+                          (v.size[0] == 1 || v.stride[0] == v.size[1] * v.size[2] * v.size[3]);
+        if (!nhwc) {
+          ensure_packed(n.in[0]);
           GNode t;
           t.op = OP_NHWC;
           t.lane = n.lane;
           t.in = {n.in[0]};
-          View4 padded = x.v;
-          padded.size[1] = cin;
-          t.out = c.new_owner(x.dtype, padded, 4);
+          t.out = c.new_owner(c.values[n.in[0]].dtype, c.values[n.in[0]].v, 4);
           sched.push_back(t);
-          n.real_cin = x.v.size[1];
           n.in[0] = t.out;
-          n.in[1] = c.reordered_filter(n.in[1], cin);
-          n.i5 = 1;
         }
+        n.conv_cin_k = cin_k;
+        n.in[1] = c.reordered_filter(n.in[1], cin_k);
+        n.i5 = 1;
         break;
       }
       default:
@@ -1602,6 +1682,27 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
       m->out_slot[outs[k]] = (int)k;
     }
     for (auto& n : m->nodes) prof_info(n, m->values);
+    // NDX_DUMP_SCHEDULE=1: the schedule on stderr, one node a line (kernel
+    // family, lane, output shape, each input's shape and strides).
+    if (const char* dump = getenv("NDX_DUMP_SCHEDULE"); dump && dump[0] == '1') {
+      auto shape = [&](int id) {
+        if (id < 0) return std::string("-");
+        const GValue& v = m->values[id];
+        char b[160];
+        snprintf(b, sizeof b, "%s[%lld,%lld,%lld,%lld]/[%lld,%lld,%lld,%lld]", dtype_name(v.dtype),
+                 (long long)v.v.size[0], (long long)v.v.size[1], (long long)v.v.size[2], (long long)v.v.size[3],
+                 (long long)v.v.stride[0], (long long)v.v.stride[1], (long long)v.v.stride[2],
+                 (long long)v.v.stride[3]);
+        return std::string(b);
+      };
+      for (size_t i = 0; i < m->nodes.size(); i++) {
+        const GNode& n = m->nodes[i];
+        std::string line = std::to_string(i) + " " + n.family + " lane" + std::to_string(n.lane) + " -> " +
+                           shape(n.out) + " <-";
+        for (int id : n.in) line += " " + shape(id);
+        fprintf(stderr, "[ndx schedule] %s\n", line.c_str());
+      }
+    }
     for (size_t i = 0; i + 1 < m->nodes.size(); i++)
       if (m->nodes[i].op == OP_LINEAR && m->nodes[i].i5 == 1) {
         m->nodes[i].flops += m->nodes[i + 1].flops;
@@ -1946,6 +2047,30 @@ struct Runner {
         break;
       }
       case OP_ROWNORM: {
+        if (n.i1) {
+          ChannelNormArgs a{};
+          const GValue& x = val(n.in[0]);
+          a.x = ptr(n.in[0]);
+          a.x_dtype = x.dtype;
+          a.y = ptr(n.out);
+          a.y_dtype = val(n.out).dtype;
+          a.N = x.v.size[0];
+          a.P = x.v.size[2];
+          a.C = x.v.size[3];
+          if (n.in[1] >= 0) {
+            a.weight = ptr(n.in[1]);
+            a.w_dtype = val(n.in[1]).dtype;
+          }
+          if (n.in[2] >= 0) {
+            a.bias = ptr(n.in[2]);
+            a.b_dtype = val(n.in[2]).dtype;
+          }
+          a.eps = n.f0;
+          a.mode = n.i0;
+          a.silu = n.i2;
+          launch_channel_norm(a, s);
+          break;
+        }
         RowNormArgs a{};
         const GValue& x = val(n.in[0]);
         const GValue& o = val(n.out);
@@ -2034,8 +2159,8 @@ struct Runner {
         a.y_dtype = o.dtype;
         a.N = (int)x.v.size[0];
         a.Cin = (int)x.v.size[1];
-        a.H = (int)x.v.size[2];
-        a.W = (int)x.v.size[3];
+        a.H = (int)x.v.size[2] << n.conv_up;
+        a.W = (int)x.v.size[3] << n.conv_up;
         a.Cout = (int)o.v.size[1];
         a.kh = n.i3;
         a.kw = n.i4;
@@ -2043,6 +2168,8 @@ struct Runner {
         a.pad = n.i1;
         a.Ho = (int)o.v.size[2];
         a.Wo = (int)o.v.size[3];
+        a.cin_k = (int)n.conv_cin_k;
+        a.up = n.conv_up;
         if (n.i5) launch_conv_gemm(a, s);
         else launch_conv2d(a, s);
         break;
@@ -2052,9 +2179,7 @@ struct Runner {
         const GValue& x = val(n.in[0]);
         const int64_t c = n.i1 ? x.v.size[3] : x.v.size[1];
         const int64_t hw = n.i1 ? x.v.size[2] : x.v.size[2] * x.v.size[3];
-        // An NHWC copy for a convolution may have more (zero) channels than x.
-        const int64_t c_pad = n.i1 ? c : val(n.out).v.size[1];
-        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], c, hw, s, c_pad);
+        launch_nchw_to_nhwc(ptr(n.in[0]), ptr(n.out), x.dtype, x.v.size[0], c, hw, s);
         break;
       }
       case OP_UPSAMPLE: {

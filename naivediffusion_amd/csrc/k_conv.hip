@@ -103,36 +103,8 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_vec_kernel(const uint16_t* x
   }
 }
 
-// The same transposition into pixel rows of c_pad > c channels, the
-// channels past c written as zeros (the implicit-GEMM convolution reads its
-// K in 64-channel tiles).
-__global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* x, uint16_t* y, int64_t c,
-                                                               int64_t c_pad, int64_t hw) {
-  __shared__ uint16_t tile[64][65];
-  const int64_t b = blockIdx.z;
-  const int64_t c0 = int64_t(blockIdx.y) * 64, p0 = int64_t(blockIdx.x) * 64;
-  const uint16_t* xb = x + b * c * hw;
-  uint16_t* yb = y + b * c_pad * hw;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t ch = c0 + r, p = p0 + tx;
-    tile[r][tx] = (ch < c && p < hw) ? xb[ch * hw + p] : uint16_t(0);
-  }
-  __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int64_t p = p0 + r, ch = c0 + tx;
-    if (ch < c_pad && p < hw) yb[p * c_pad + ch] = tile[tx][r];
-  }
-}
-
-void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s,
-                         int64_t c_pad) {
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s) {
   if (dtype_size(dtype) != 2) throw std::runtime_error("nchw_to_nhwc: 16-bit elements only");
-  if (c_pad > c) {
-    dim3 g((unsigned)((hw + 63) / 64), (unsigned)((c_pad + 63) / 64), (unsigned)n);
-    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, c_pad, hw);
-    return;
-  }
   dim3 g((unsigned)((hw + 63) / 64), (unsigned)((c + 63) / 64), (unsigned)n);
   if (c % 64 == 0 && hw % 64 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0) {
     hipLaunchKernelGGL(nchw_to_nhwc_vec_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, hw);

@@ -516,7 +516,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   const T* A = (const T*)a.a + bidx * a.batch_a;
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)((int64_t(a.M - 1) * a.lda + a.K) * ES));
   const __amdgpu_buffer_rsrc_t rw =
-      CONV ? make_rsrc((const T*)a.w + bidx * a.batch_w, (uint32_t)(int64_t(a.conv_h) * a.conv_w * a.conv_cin * ES))
+      CONV ? make_rsrc((const T*)a.w + bidx * a.batch_w,
+                       (uint32_t)(int64_t(a.conv_h >> a.conv_up) * (a.conv_w >> a.conv_up) * a.conv_c * ES))
            : make_rsrc(a.w, (uint32_t)((int64_t(a.N - 1) * a.ldw + a.K) * ES));
 
   // Lane l of a kilobyte load: row (l / 8) of its 8-row group, physical
@@ -574,19 +575,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
       }
     }
     if constexpr (CONV) {
-      // A K tile lies within one tap (Cin is a multiple of BK): (ky, kx)
-      // and the channel offset are uniform over the workgroup.
+      // A K tile lies within one tap (conv_cin is a multiple of BK): (ky,
+      // kx) and the channel offset are uniform over the workgroup. An
+      // 8-channel chunk at or past conv_c (a multiple of 8) reads zeros;
+      // through the upsample, pixel (iy, ix) is stored at (iy / 2, ix / 2).
       const int k0 = kt * BK;
       const int tap = k0 / a.conv_cin;
       const int ci0 = k0 - tap * a.conv_cin;
       const int ky = tap / a.conv_kw, kx = tap - ky * a.conv_kw;
+      const int up = a.conv_up, row_w = a.conv_w >> up;
 #pragma unroll
       for (int i = 0; i < B_LOADS; i++) {
         const int q = (wave * B_LOADS + i) & 1;
-        const int iy = pix_y[i] + ky, ix = pix_x[i] + kx;
-        const bool in = kin[q] && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
-        const uint32_t off =
-            in ? uint32_t(((iy * a.conv_w + ix) * a.conv_cin + ci0 + kchunk_q[q] * 8) * ES) : kOutOfRange;
+        const int iy = pix_y[i] + ky, ix = pix_x[i] + kx, ci = ci0 + kchunk_q[q] * 8;
+        const bool in =
+            kin[q] && ci < a.conv_c && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
+        const uint32_t off = in ? uint32_t((((iy >> up) * row_w + (ix >> up)) * a.conv_c + ci) * ES) : kOutOfRange;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0, 0);
       }
     } else if constexpr (KFULL) {
@@ -1479,17 +1483,17 @@ static ConvKind conv_choose(const GemmArgs& g) {
 static GemmArgs conv_gemm_args(const ConvArgs& c) {
   GemmArgs g{};
   const int taps = c.kh * c.kw;
-  g.a = c.w; g.lda = int64_t(taps) * c.Cin; g.batch_a = 0; g.a_dtype = c.x_dtype;
-  g.w = c.x; g.ldw = 0; g.batch_w = int64_t(c.H) * c.W * c.Cin; g.w_dtype = c.x_dtype;
+  g.a = c.w; g.lda = int64_t(taps) * c.cin_k; g.batch_a = 0; g.a_dtype = c.x_dtype;
+  g.w = c.x; g.ldw = 0; g.batch_w = int64_t(c.H >> c.up) * (c.W >> c.up) * c.Cin; g.w_dtype = c.x_dtype;
   g.c = c.y; g.ldc = int64_t(c.Ho) * c.Wo; g.batch_c = int64_t(c.Cout) * c.Ho * c.Wo; g.c_dtype = c.y_dtype;
   g.row_bias = c.bias; g.row_bias_dtype = c.bias_dtype;
   if (c.resid) {
     g.resid = c.resid; g.ldr = g.ldc; g.batch_r = g.batch_c; g.r_dtype = c.y_dtype;
     g.epilogue = EPI_RESIDUAL;
   }
-  g.M = c.Cout; g.N = c.Ho * c.Wo; g.K = taps * c.Cin; g.batch = c.N;
-  g.conv_cin = c.Cin; g.conv_h = c.H; g.conv_w = c.W; g.conv_wo = c.Wo; g.conv_kw = c.kw;
-  g.conv_stride = c.stride; g.conv_pad = c.pad;
+  g.M = c.Cout; g.N = c.Ho * c.Wo; g.K = taps * c.cin_k; g.batch = c.N;
+  g.conv_cin = c.cin_k; g.conv_c = c.Cin; g.conv_h = c.H; g.conv_w = c.W; g.conv_wo = c.Wo; g.conv_kw = c.kw;
+  g.conv_stride = c.stride; g.conv_pad = c.pad; g.conv_up = c.up;
   return g;
 }
 
@@ -1503,6 +1507,8 @@ const char* conv_family(const ConvArgs& c) {
 }
 
 void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
+  if (c.cin_k % BK || c.cin_k < c.Cin || c.Cin % 8 || (c.up && (c.H % 2 || c.W % 2)))
+    throw std::runtime_error("conv_gemm: channels per tap must be a multiple of 64 covering a multiple of 8");
   const GemmArgs g = conv_gemm_args(c);
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   switch (conv_choose(g)) {

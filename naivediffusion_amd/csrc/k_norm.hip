@@ -1,9 +1,11 @@
 // Wavefront-reduction normalisation kernels: LayerNorm (+affine),
 // Transformer.Modulate (LayerNorm * (1 + scale) + shift, cast), RMSNorm,
-// the per-head RMSNorm + rotate-half RoPE of the attention inputs, and
-// GroupNorm (+affine, +SiLU).
+// the same norms over the channels of an NCHW image written as tokens
+// (+SiLU), the per-head RMSNorm + rotate-half RoPE of the attention inputs,
+// and GroupNorm (+affine, +SiLU).
 
 #include <algorithm>
+#include <stdexcept>
 
 #include "k_common.h"
 
@@ -371,6 +373,269 @@ void launch_row_norm(const RowNormArgs& a, hipStream_t s) {
   else if (vpt <= 48) hipLaunchKernelGGL(row_norm_kernel<48>, grid, block, 0, s, a);
   else if (vpt <= 64) hipLaunchKernelGGL(row_norm_kernel<64>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(row_norm_wide_kernel, dim3((unsigned)a.rows), block, 0, s, a);
+}
+
+// The row norm of the token view of a packed NCHW image, written as packed
+// tokens. A workgroup owns 64 pixels of one image; lane l of every wave
+// holds pixel l, so each load of a wave is 64 consecutive pixels of one
+// channel. Pass 1: wave w sums channels w, w + 4, ... and the four partial
+// sums meet in LDS (a LayerNorm re-reads for the squared deviations). Pass 2
+// re-reads 64-channel slabs, normalises them into an LDS tile
+// [pixel][channel], and writes each pixel's slab as one contiguous run.
+__global__ __launch_bounds__(256) void channel_norm_kernel(ChannelNormArgs a) {
+  __shared__ float red[2][4][64];
+  __shared__ float tile[64][65];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t C = a.C, P = a.P;
+  const int64_t n = blockIdx.y, p0 = int64_t(blockIdx.x) * 64, p = p0 + lane;
+  const bool live = p < P;
+  const int64_t xb = n * C * P + p;
+  float s = 0.f, ss = 0.f;
+  if (live) {
+#pragma unroll 8
+    for (int64_t c = w; c < C; c += 4) {
+      const float v = load_f(a.x, a.x_dtype, xb + c * P);
+      s += v;
+      ss += v * v;
+    }
+  }
+  red[0][w][lane] = s;
+  red[1][w][lane] = ss;
+  __syncthreads();
+  s = red[0][0][lane] + red[0][1][lane] + red[0][2][lane] + red[0][3][lane];
+  ss = red[1][0][lane] + red[1][1][lane] + red[1][2][lane] + red[1][3][lane];
+  float mean = 0.f, rstd;
+  if (a.mode == 2) {
+    rstd = 1.0f / sqrtf(ss / C + a.eps);
+  } else {
+    mean = s / C;
+    float q = 0.f;
+    if (live) {
+#pragma unroll 8
+      for (int64_t c = w; c < C; c += 4) {
+        const float d = load_f(a.x, a.x_dtype, xb + c * P) - mean;
+        q += d * d;
+      }
+    }
+    __syncthreads();
+    red[0][w][lane] = q;
+    __syncthreads();
+    q = red[0][0][lane] + red[0][1][lane] + red[0][2][lane] + red[0][3][lane];
+    rstd = 1.0f / sqrtf(q / C + a.eps);
+  }
+  const int64_t yb = (n * P + p0) * C;
+  for (int64_t c0 = 0; c0 < C; c0 += 64) {
+#pragma unroll 4
+    for (int j = w; j < 64; j += 4) {
+      const int64_t c = c0 + j;
+      float y = 0.f;
+      if (live && c < C) {
+        y = (load_f(a.x, a.x_dtype, xb + c * P) - mean) * rstd;
+        if (a.weight) y *= load_f(a.weight, a.w_dtype, c);
+        if (a.bias) y += load_f(a.bias, a.b_dtype, c);
+        if (a.silu) y = silu_f(round_to(y, a.y_dtype));
+      }
+      tile[lane][j] = y;
+    }
+    __syncthreads();
+    const int64_t cols = C - c0 < 64 ? C - c0 : 64;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      const int px = i >> 6, cc = i & 63;
+      if (cc < cols && p0 + px < P) store_f(a.y, a.y_dtype, yb + px * C + c0 + cc, tile[px][cc]);
+    }
+    __syncthreads();
+  }
+}
+
+// Eight 16-bit values from 16 bytes, as floats.
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4 u, float v[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if constexpr (__is_same(T, __bf16)) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      const _Float16* h = (const _Float16*)&w[i];
+      v[2 * i] = (float)h[0];
+      v[2 * i + 1] = (float)h[1];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float half_to_f(uint16_t h) {
+  if constexpr (__is_same(T, __bf16)) return bf16_bits_to_f32(h);
+  else return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// channel_norm_kernel for 16-bit images whose channels and pixels are
+// multiples of 8, with 16-byte accesses on both sides. A workgroup of
+// THREADS owns 64 pixels; thread t holds the eight pixels 8 (t % 8) ..
+// 8 (t % 8) + 7 and the channels t / 8 + ROWS r (ROWS = THREADS / 8 rows a
+// pass), so eight lanes read one channel's 128 contiguous bytes and a wave
+// eight channels per load. With RPT > 0 (RMSNorm, C <= ROWS RPT) a thread
+// keeps its RPT channel rows in registers from the statistics to the
+// output and the image is read once; with RPT = 0 it is read again (and a
+// LayerNorm a third time, for the squared deviations). The statistics meet
+// across a pixel group's lanes by shuffles and across the waves in LDS; the
+// output pass stages ROWS-channel slabs in LDS [channel][pixel] and writes
+// eight channels of a pixel per 16-byte store.
+template <typename T, int RPT, int THREADS>
+__global__ __launch_bounds__(THREADS) void channel_norm_vec_kernel(ChannelNormArgs a) {
+  constexpr int WAVES = THREADS / 64, ROWS = THREADS / 8, PER_PX = ROWS / 8;
+  __shared__ float red[2][WAVES][64];
+  __shared__ float stat[2][64];
+  __shared__ __align__(16) uint16_t tile[ROWS][66];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = t & 7, row = t >> 3;
+  const int64_t C = a.C, P = a.P;
+  const int64_t n = blockIdx.y, p0 = int64_t(blockIdx.x) * 64;
+  const bool live = p0 + 8 * g < P;  // P is a multiple of 8: a group is whole or past the end
+  const T* x = (const T*)a.x + n * C * P + p0 + 8 * g;
+  auto load_row = [&](int64_t c) {
+    return live && c < C ? *(const uint4*)(x + c * P) : make_uint4(0, 0, 0, 0);
+  };
+
+  // Sums of the eight pixels over this wave's lanes that hold them, then
+  // into red[which][wave].
+  auto reduce_groups = [&](float v[8], int which) {
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+#pragma unroll
+      for (int o = 8; o < 64; o <<= 1) v[e] += __shfl_xor(v[e], o, 64);
+    if (lane < 8)
+#pragma unroll
+      for (int e = 0; e < 8; e++) red[which][w][8 * lane + e] = v[e];
+  };
+  auto total = [&](int which) {
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < WAVES; i++) v += red[which][i][t];
+    return v;
+  };
+
+  uint4 keep[RPT > 0 ? RPT : 1];
+  if constexpr (RPT > 0) {
+#pragma unroll
+    for (int r = 0; r < RPT; r++) keep[r] = load_row(row + ROWS * r);
+  }
+  float s[8], ss[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) s[e] = ss[e] = 0.f;
+  auto accumulate = [&](const uint4 u) {
+    float v[8];
+    unpack8<T>(u, v);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      s[e] += v[e];
+      ss[e] += v[e] * v[e];
+    }
+  };
+  if constexpr (RPT > 0) {
+#pragma unroll
+    for (int r = 0; r < RPT; r++) accumulate(keep[r]);  // rows past C hold zeros
+  } else if (live) {
+#pragma unroll 4
+    for (int64_t c = row; c < C; c += ROWS) accumulate(*(const uint4*)(x + c * P));
+  }
+  reduce_groups(s, 0);
+  reduce_groups(ss, 1);
+  __syncthreads();
+  if (t < 64) {
+    stat[0][t] = a.mode == 2 ? 0.f : total(0) / C;
+    stat[1][t] = 1.0f / sqrtf(total(1) / C + a.eps);
+  }
+  __syncthreads();
+  if constexpr (RPT == 0) {
+    if (a.mode != 2) {
+      // LayerNorm: the squared deviations from the mean.
+      float m[8], q[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        m[e] = stat[0][8 * g + e];
+        q[e] = 0.f;
+      }
+      if (live) {
+#pragma unroll 4
+        for (int64_t c = row; c < C; c += ROWS) {
+          float v[8];
+          unpack8<T>(*(const uint4*)(x + c * P), v);
+#pragma unroll
+          for (int e = 0; e < 8; e++) q[e] += (v[e] - m[e]) * (v[e] - m[e]);
+        }
+      }
+      reduce_groups(q, 0);
+      __syncthreads();
+      if (t < 64) stat[1][t] = 1.0f / sqrtf(total(0) / C + a.eps);
+      __syncthreads();
+    }
+  }
+
+  // Channels c0 .. c0 + ROWS - 1, thread row `row` holding u.
+  T* y = (T*)a.y + (n * P + p0) * C;
+  auto slab = [&](int64_t c0, const uint4 u) {
+    uint32_t* d = (uint32_t*)&tile[row][8 * g];
+    d[0] = u.x;
+    d[1] = u.y;
+    d[2] = u.z;
+    d[3] = u.w;
+    __syncthreads();
+    const int px = t / PER_PX, cc = (t % PER_PX) * 8;
+    const int64_t c = c0 + cc;
+    if (c < C && p0 + px < P) {
+      const float mean = stat[0][px], rstd = stat[1][px];
+      __align__(16) T out[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float v = (half_to_f<T>(tile[cc + e][px]) - mean) * rstd;
+        if (a.weight) v *= load_f(a.weight, a.w_dtype, c + e);
+        if (a.bias) v += load_f(a.bias, a.b_dtype, c + e);
+        if (a.silu) v = silu_f((float)(T)v);
+        out[e] = (T)v;
+      }
+      *(uint4*)(y + px * C + c) = *(const uint4*)out;
+    }
+    __syncthreads();
+  };
+  if constexpr (RPT > 0) {
+#pragma unroll
+    for (int r = 0; r < RPT; r++)
+      if (ROWS * r < C) slab(ROWS * r, keep[r]);
+  } else {
+    for (int64_t c0 = 0; c0 < C; c0 += ROWS) slab(c0, load_row(c0 + row));
+  }
+}
+
+void launch_channel_norm(const ChannelNormArgs& a, hipStream_t s) {
+  if (a.N == 0 || a.P == 0 || a.C == 0) return;
+  if (a.N > 65535 || a.mode == 1) throw std::runtime_error("channel_norm: up to 65535 images, LayerNorm or RMSNorm");
+  dim3 grid((unsigned)((a.P + 63) / 64), (unsigned)a.N);
+  const bool half = (a.x_dtype == NDX_BF16 || a.x_dtype == NDX_F16) && a.y_dtype == a.x_dtype;
+  if (half && a.C % 8 == 0 && a.P % 8 == 0 && (uintptr_t)a.x % 16 == 0 && (uintptr_t)a.y % 16 == 0) {
+#define NDX_CHANNEL_NORM(RPT, THREADS)                                                                        \
+  do {                                                                                                       \
+    if (a.x_dtype == NDX_BF16)                                                                               \
+      hipLaunchKernelGGL((channel_norm_vec_kernel<__bf16, RPT, THREADS>), grid, dim3(THREADS), 0, s, a);      \
+    else                                                                                                     \
+      hipLaunchKernelGGL((channel_norm_vec_kernel<_Float16, RPT, THREADS>), grid, dim3(THREADS), 0, s, a);    \
+    return;                                                                                                  \
+  } while (0)
+    // An RMSNorm keeps each thread's rows in registers: up to ten 16-byte
+    // rows, the workgroup widened to 512 threads for wider images. Wider
+    // still, 1024 threads re-read (ten rows would not fit their registers).
+    if (a.mode == 2) {
+      if (a.C <= 64) NDX_CHANNEL_NORM(2, 256);
+      if (a.C <= 128) NDX_CHANNEL_NORM(4, 256);
+      if (a.C <= 192) NDX_CHANNEL_NORM(6, 256);
+      if (a.C <= 320) NDX_CHANNEL_NORM(10, 256);
+      if (a.C <= 640) NDX_CHANNEL_NORM(10, 512);
+    }
+    if (a.C > 320) NDX_CHANNEL_NORM(0, 1024);
+    NDX_CHANNEL_NORM(0, 256);
+#undef NDX_CHANNEL_NORM
+  }
+  hipLaunchKernelGGL(channel_norm_kernel, grid, dim3(256), 0, s, a);
 }
 
 // One wave per (batch, token, head): RMSNorm of the head's d features with

@@ -101,10 +101,12 @@ struct GemmArgs {
   // where rows are output channels).
   const void* row_bias; int row_bias_dtype;
   // Implicit-GEMM convolution: with conv_cin > 0 the weight operand's row n
-  // is output pixel n, gathered from an NHWC input [batch, H, W, Cin] (w,
+  // is output pixel n, gathered from an NHWC input [batch, H, W, conv_c] (w,
   // batch_w elements per image) at taps (ky, kx) of a kw-wide filter whose
-  // K index is (ky * kw + kx) * Cin + ci.
-  int conv_cin, conv_h, conv_w, conv_wo, conv_kw, conv_stride, conv_pad;
+  // K index is (ky * kw + kx) * conv_cin + ci; channels ci at or past conv_c
+  // read as zero. With conv_up the input is read through a nearest 2x
+  // upsample: conv_h x conv_w is the upsampled size, memory holds half.
+  int conv_cin, conv_c, conv_h, conv_w, conv_wo, conv_kw, conv_stride, conv_pad, conv_up;
   // The 16-bit tile to use regardless of the latency model (0: the model;
   // 1..4: 256x256, 128x128, 64x128, 64x64).
   int tile_hint;
@@ -182,13 +184,35 @@ struct GroupNormArgs {
 int group_norm_splits(int64_t count);
 
 struct ConvArgs {
-  const void* x; int x_dtype;  // [N, Cin, H, W] packed
-  const void* w; int w_dtype;  // [Cout, Cin, kh, kw] packed (or int8 + scales)
+  // [N, Cin, H, W] packed; NHWC ([N, H, W, Cin] packed) for the implicit GEMM
+  const void* x; int x_dtype;
+  // [Cout, Cin, kh, kw] packed (or int8 + scales); [Cout, kh, kw, cin_k]
+  // for the implicit GEMM
+  const void* w; int w_dtype;
   const void* scales; int qblock; int s_dtype;
   const void* bias; int bias_dtype;
   const void* resid;           // [N, Cout, Ho, Wo] packed, same dtype as y
   void* y; int y_dtype;
   int N, Cin, H, W, Cout, kh, kw, stride, pad, Ho, Wo;
+  // Implicit GEMM only: the filter's channels per tap (Cin rounded up to a
+  // multiple of 64, zeros past Cin), and whether x is read through a nearest
+  // 2x upsample (H x W the upsampled size; x holds H/2 x W/2 pixels).
+  int cin_k, up;
+};
+
+// A norm over the channels of packed NCHW [N, C, P] written as packed tokens
+// [N, P, C]: the row norm (LayerNorm, mode 0, or RMSNorm, mode 2) of the
+// token view of an image without a transposed copy first, the result
+// optionally passed through SiLU (rounded to y's type before and after).
+struct ChannelNormArgs {
+  const void* x; int x_dtype;
+  void* y; int y_dtype;
+  int64_t N, C, P;
+  const void* weight; int w_dtype;  // [C] or null
+  const void* bias; int b_dtype;    // [C] or null
+  float eps;
+  int mode;
+  int silu;
 };
 
 // Generic strided elementwise: out = f(in0, in1) over a 4-D shape.
@@ -233,16 +257,17 @@ void launch_group_norm(const GroupNormArgs& a, hipStream_t s);
 // dtype (F32, BF16 or F16) in and out.
 void launch_softmax(const void* x, void* y, int dtype, int64_t rows, int64_t cols, float scale, hipStream_t s);
 void launch_conv2d(const ConvArgs& a, hipStream_t s);
-// The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, Cin]
-// (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types,
-// Cin a multiple of 64. conv_gemm_cin is the channel count the GEMM runs
-// with: Cin itself, Cin rounded up to a multiple of 64 (the NHWC copy and the
-// filter padded with zero channels) where that adds at most half, or 0 when
-// the direct kernel should run instead.
+void launch_channel_norm(const ChannelNormArgs& a, hipStream_t s);
+// The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, cin_k]
+// (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types.
+// conv_gemm_cin is the K channel count per tap the GEMM runs with: Cin
+// itself for a multiple of 64, Cin rounded up to one (the filter padded
+// with zero channels, the input's missing channels read as zeros) where
+// that adds at most half and Cin is a multiple of 8, else 0: the direct
+// kernel runs instead.
 int64_t conv_gemm_cin(int x_dtype, int w_dtype, int64_t cin);
 void launch_conv_gemm(const ConvArgs& a, hipStream_t s);
-void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s,
-                         int64_t c_pad = 0);
+void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s);
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
                            hipStream_t s, int64_t cin_pad = 0);
 const char* conv_family(const ConvArgs& a);

@@ -58,8 +58,8 @@ CASES = [
     (2, 640, 8, 8, 1280, 3, 1, 1),
     (1, 192, 9, 31, 96, 3, 1, 1),
     # Channel counts that are multiples of 8 but not of 64 (the Wan VAE's
-    # 144 and 288): the NHWC copy and the filter padded with zero channels
-    # to 192 and 320.
+    # 144 and 288): the filter padded with zero channels to 192 and 320, the
+    # input's missing channels read as zeros.
     (1, 144, 13, 11, 144, 3, 1, 1),
     (2, 288, 7, 9, 144, 1, 1, 0),
     (1, 288, 10, 6, 576, 3, 2, 1),
@@ -94,6 +94,58 @@ def test_conv_residual_is_fused(device):
     out, families = run_conv(device, dtype, x, w, b, 1, 1, residual=r)
     assert rel_err(out, oracle.conv2d(x, w, b, 1, 1) + r) <= TOL[dtype]
     assert any(f.startswith("conv_mfma_") for f in families), families
+
+
+def run_graph(device, dtype, build, *arrays):
+    model = nd.ModelBuilder(device, dtype)
+    ins = [model.Placeholder(list(a.shape), dtype) for a in arrays]
+    model.Compile([build(model, *ins)])
+    model.Compiled.SetProfiling(True)
+    out = model.Run(*[HostTensor.FromFloats(a).ConvertTo(dtype) for a in arrays])[0].ToFloats()
+    families = set(model.Compiled.Profile())
+    model.Dispose()
+    return out, families
+
+
+@pytest.mark.parametrize("B,C,H,W,Cout", [(1, 128, 12, 10, 64), (2, 144, 9, 7, 96), (1, 288, 6, 11, 288)])
+def test_conv_reads_token_rows_in_place(device, B, C, H, W, Cout):
+    """A convolution of ToImage(tokens) (an NHWC image: what a norm over
+    channels leaves) reads the token rows as they lie, with no transposed
+    copy; 144 and 288 channels have their last K slab part zeros."""
+    dtype = DT.BFloat16
+    print(f"[gpu] conv of token rows {B}x{H * W}x{C} -> {Cout}", flush=True)
+    t = narrow(normal("tr_t", (B, 1, H * W, C)), dtype)
+    w = narrow(normal("tr_w", (Cout, C, 3, 3), 1.0 / np.sqrt(C * 9)), dtype)
+    b = narrow(normal("tr_b", (Cout,), 0.1), dtype)
+    out, families = run_graph(device, dtype, lambda m, ti: Layers.Conv2d(
+        m, Layers.ToImage(ti, H, W), HostTensor.FromFloats(w), HostTensor.FromFloats(b), 1, 1), t)
+    x = np.ascontiguousarray(t.reshape(B, H, W, C).transpose(0, 3, 1, 2))
+    err = rel_err(out, oracle.conv2d(x, w, b, 1, 1))
+    print(f"[gpu]   rel err {err:.2e} via {sorted(families)}", flush=True)
+    assert err <= TOL[dtype]
+    assert any(f.startswith("conv_mfma_") for f in families), families
+    assert "nchw_to_nhwc" not in families and "elementwise" not in families, families
+
+
+@pytest.mark.parametrize("B,C,H,W,Cout,k,stride,pad", [
+    (1, 128, 7, 5, 64, 3, 1, 1), (2, 144, 6, 9, 144, 3, 1, 1), (1, 64, 8, 8, 128, 1, 1, 0),
+    (1, 64, 5, 6, 64, 3, 2, 1)])
+def test_conv_reads_through_a_fused_upsample(device, B, C, H, W, Cout, k, stride, pad):
+    """Conv2d(UpsampleNearest(x)) (the decoders' upsamplers) never writes
+    the upsampled image: the convolution reads pixel (y, x) of it from
+    (y / 2, x / 2) of its source."""
+    dtype = DT.BFloat16
+    print(f"[gpu] conv through upsample {B}x{C}x{H}x{W} -> {Cout} k{k} s{stride}", flush=True)
+    x = narrow(normal("up_x", (B, C, H, W)), dtype)
+    w = narrow(normal("up_w", (Cout, C, k, k), 1.0 / np.sqrt(C * k * k)), dtype)
+    b = narrow(normal("up_b", (Cout,), 0.1), dtype)
+    out, families = run_graph(device, dtype, lambda m, xi: Layers.Conv2d(
+        m, Layers.UpsampleNearest(xi), HostTensor.FromFloats(w), HostTensor.FromFloats(b), stride, pad), x)
+    up = np.repeat(np.repeat(x, 2, 2), 2, 3)
+    err = rel_err(out, oracle.conv2d(up, w, b, stride, pad))
+    print(f"[gpu]   rel err {err:.2e} via {sorted(families)}", flush=True)
+    assert err <= TOL[dtype]
+    assert "upsample" not in families and any(f.startswith("conv_mfma_") for f in families), families
 
 
 @pytest.mark.parametrize("tile", ["256", "128", "64x128", "64x64"])

@@ -862,3 +862,49 @@ def test_layer_and_rms_norm_16bit(device, dtype, D):
     o1, o2 = run(model, HostTensor.FromFloats(x).ConvertTo(dtype))
     assert rel_err(o1.reshape(rows, D), oracle.layer_norm(x.reshape(rows, D), w, b, 1e-5)) <= BF16_TOL
     assert rel_err(o2.reshape(rows, D), oracle.rms_norm(x.reshape(rows, D), w, 1e-6)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float16, DT.Float32])
+@pytest.mark.parametrize("shape", [(1, 144, 9, 13), (1, 1152, 5, 7), (2, 64, 8, 8), (1, 96, 8, 12),
+                                   (1, 144, 8, 12), (1, 288, 4, 10), (1, 576, 4, 6), (2, 1152, 4, 18)])
+@pytest.mark.parametrize("silu", [False, True])
+def test_channel_norm_of_an_image(device, dtype, shape, silu):
+    """RMSNorm and LayerNorm of an NCHW image's token view (the Wan VAE's
+    channel norms) run on the image as it lies and write tokens, a SiLU
+    after them joined in: no transposed copy, no separate SiLU pass. Against
+    the oracle's row norms of the transposed image, the SiLU taken of the
+    norm rounded to the compute type (what the unfused graph computes).
+    Channel counts above and below one 64-channel slab, pixels not a
+    multiple of 64, two images. 16-bit images whose pixels are a multiple
+    of 8 take the 16-byte kernel (each register-held width of the RMSNorm,
+    256 and 512 threads, and the re-reading form at 256 and 1024 threads),
+    the rest the per-element one."""
+    B, C, H, W = shape
+    print(f"[gpu] channel norm {dtype.name} {shape} silu={silu}", flush=True)
+    x = _round(normal("cn_x", shape) * 2 + 0.5, dtype)
+    w = _round(normal("cn_w", (C,), 0.3) + 1, dtype)
+    b = _round(normal("cn_b", (C,), 0.3), dtype)
+    model = nd.ModelBuilder(device, dtype)
+    xi = model.Placeholder(list(shape), dtype)
+    t = Layers.ToTokens(xi)
+    rms = Layers.RmsNorm(model, t, HostTensor.FromFloats(w), 1e-6)
+    ln = Layers.LayerNorm(model, t, HostTensor.FromFloats(w), HostTensor.FromFloats(b), 1e-5)
+    if silu:
+        rms, ln = Layers.Silu(rms), Layers.Silu(ln)
+    model.Compile([rms, ln])
+    model.Compiled.SetProfiling(True)
+    host = HostTensor.FromFloats(x)
+    o1, o2 = run(model, host if dtype == DT.Float32 else host.ConvertTo(dtype))
+    families = set(model.Compiled.Profile())
+    model.Dispose()
+    rows = x.transpose(0, 2, 3, 1).reshape(B * H * W, C)
+    want = [oracle.rms_norm(rows, w, 1e-6), oracle.layer_norm(rows, w, b, 1e-5)]
+    if silu:
+        want = [(lambda v: v / (1.0 + np.exp(-v)))(_round(r, dtype)) for r in want]
+    tol = 1e-5 if dtype == DT.Float32 else 1e-2
+    for got, ref in zip((o1, o2), want):
+        err = rel_err(got.reshape(ref.shape), ref)
+        print(f"[gpu]   rel err {err:.2e}", flush=True)
+        assert err <= tol
+    assert {"channel_rms_norm", "channel_layer_norm"} <= families, families
+    assert "nchw_to_nhwc" not in families and "elementwise" not in families, families
