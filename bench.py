@@ -224,7 +224,8 @@ def setup_mmdit(args, dev, seed, DT):
     t0 = time.perf_counter()
     weights = mmdit.device_weights(dev, cfg, seed)
     log(f"synthetic weights on the device in {time.perf_counter() - t0:.1f} s")
-    model = mmdit.build_step_model(dev, cfg, weights, B, nt, lat_h, lat_w, compute, args.int8)
+    model = mmdit.build_step_model(dev, cfg, weights, B, nt, lat_h, lat_w, compute, args.int8,
+                                   two_streams=not args.one_stream)
     n = ni + nt
     cos, sin = mmdit.rope_tables(gh, gw, nt)
     temb = np.tile(mmdit.time_embedding(0.5, cfg.time_dim), (B, 1)).reshape(B, 1, 1, cfg.time_dim)
@@ -245,7 +246,8 @@ def setup_mmdit(args, dev, seed, DT):
                              f"{img_h}x{img_w} (latent 16x{lat_h}x{lat_w}, 2x2 patch: {ni} image + {nt} text tokens), "
                              f"hidden 3072, 24x128 heads, MLP 12288, batch {B}, {args.compute} compute, {wdesc}"),
                 "blocks": cfg.blocks, "image_tokens": ni, "text_tokens": nt, "batch": B,
-                "weights": f"int8-{args.int8}" if args.int8 else args.compute},
+                "weights": f"int8-{args.int8}" if args.int8 else args.compute,
+                "streams": 1 if args.one_stream else 2},
         data="synthetic (seeded N(0,1) latent and text, N(0,0.02) bf16 weights made on the GPU)",
         cpu=lambda: cpu_baseline(dev, cfg, seed, ni, nt, (gh, gw), B),
     )
@@ -451,6 +453,8 @@ def main():
     ap.add_argument("--image", default="1024x1344", help="mmdit: image size HxW (1328x1328 with --batch 2 and "
                     "--int8 channel is the CFG int8 configuration)")
     ap.add_argument("--batch", type=int, default=1, help="mmdit: batch (2: cond + uncond CFG)")
+    ap.add_argument("--one-stream", action="store_true", help="mmdit: the text stream on the image stream's "
+                    "stream (default: its own, beside the image stream)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")
     args = ap.parse_args()

@@ -94,7 +94,14 @@ int64_t numel4(const View4& v) { return v.size[0] * v.size[1] * v.size[2] * v.si
 // tiles do the same work in about two thirds of the CU time of 64x64 ones
 // (the MMDiT text stream: 2% less step time on MI355X; 256x256 tiles hold
 // CUs so long that the other stream's rounds stall).
-int second_stream_tile(const GNode& n, int64_t rows) { return n.lane == 1 && rows >= 128 ? 2 : 0; }
+// NDX_SECOND_STREAM_TILE=1..4 (256x256, 128x128, 64x128, 64x64) pins it,
+// read at compile time, for sweeps.
+int second_stream_tile(const GNode& n, int64_t rows) {
+  if (n.lane != 1 || rows < 128) return 0;
+  if (const char* pin = getenv("NDX_SECOND_STREAM_TILE"); pin && pin[0] >= '1' && pin[0] <= '4' && !pin[1])
+    return pin[0] - '0';
+  return 2;
+}
 
 View4 packed4(const int64_t* size) {
   View4 v;
