@@ -78,6 +78,9 @@ struct GNode {
   // read through a nearest 2x upsample (a fused UpsampleNearest).
   int64_t conv_cin_k = 0;
   int conv_up = 0;
+  // A linear's tile fixed at compile time (1..4 as GemmArgs::tile_hint; 0:
+  // the second stream's choice or the latency model's).
+  int tile_hint = 0;
   // the stream (0 the device's, 1 the second) the node runs on
   int lane = 0;
   // profiling
@@ -1505,6 +1508,149 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     n = fused;
   }
 
+  // Off unless NDX_FUSE_QK_NORM=1 (read at compile time): on the MMDiT
+  // step the fused epilogue costs the 256x256 QKV product more (383 against
+  // 310 us a launch) than the two head-norm passes it removes (27 us).
+  const char* fuse_qk_env = getenv("NDX_FUSE_QK_NORM");
+  const bool fuse_qk = fuse_qk_env && fuse_qk_env[0] == '1';
+  // Rewrite: the head norm + rotation of the q and k thirds of a QKV
+  // projection (Rotate(HeadNorm(Linear(x))), QwenImageDit.cs:342-347;
+  // Transformer.cs:37-64) runs in the projection's epilogue
+  // (EPI_QK_NORM_ROPE): the two head-norm nodes' outputs become views of
+  // the projection's q and k columns and the nodes never run. It applies
+  // when the projection's output is read only by those two and through
+  // views of its v third, the heads are 128 wide, and the tile the product
+  // runs on can hold a head pair in its epilogue.
+  for (size_t li = 0; li < src.size() && fuse_qk; li++) {
+    GNode& L = src[li];
+    if (L.op != OP_LINEAR || L.i0 != EPI_NONE || L.in.size() != 5 || L.in[3] >= 0 || L.in[4] >= 0) continue;
+    const int lo = L.out;
+    const GValue& ov = c.values[lo];
+    const GValue& wv = c.values[L.in[1]];
+    const int64_t N = wv.v.size[2], rows = ov.v.size[2];
+    if (ov.kind != VK_NODE || ov.base != lo || N % 3 || (N / 3) % 128 || !is_packed(ov.v) || ov.v.size[3] != N) continue;
+    if (std::find(outs.begin(), outs.end(), lo) != outs.end()) continue;
+    const int64_t D = N / 3;
+    int hnr[2] = {-1, -1};
+    bool ok = true;
+    // A view of lo within the v third: whole rows of N, columns [2D, 3D).
+    auto in_v = [&](int id) {
+      const GValue& v = c.values[id];
+      const int64_t c0 = v.offset % N;
+      return v.v.stride[3] == 1 && (v.v.size[2] <= 1 || v.v.stride[2] == N) && c0 >= 2 * D &&
+             c0 + v.v.size[3] <= N;
+    };
+    for (size_t ni = 0; ni < src.size() && ok; ni++) {
+      const GNode& u = src[ni];
+      std::vector<int> reads(u.in.begin(), u.in.end());
+      if (u.op == OP_ATTN)
+        for (int j = 0; j < 3; j++) reads.insert(reads.end(), {u.seg[j][0], u.seg[j][1]});
+      for (size_t k = 0; k < reads.size(); k++) {
+        const int id = reads[k];
+        if (id < 0 || c.values[id].base != lo || (int)ni == (int)li) continue;
+        if (u.op == OP_HNR && k == 0) {
+          const GValue& x = c.values[id];
+          const int which = x.offset == 0 ? 0 : x.offset == D ? 1 : -1;
+          if (which < 0 || hnr[which] >= 0 || x.v.size[3] != D || x.v.stride[3] != 1 || x.v.size[2] != rows ||
+              x.v.stride[2] != N)
+            ok = false;
+          else
+            hnr[which] = (int)ni;
+        } else if (!in_v(id)) {
+          ok = false;
+        }
+      }
+    }
+    for (int o : outs)
+      if (c.values[o].base == lo && !in_v(o)) ok = false;
+    if (!ok || hnr[0] < 0 || hnr[1] < 0) continue;
+    const GNode& hq = src[hnr[0]];
+    const GNode& hk = src[hnr[1]];
+    auto same_dtype = [&](int a, int b) {
+      return (a < 0 && b < 0) || (a >= 0 && b >= 0 && c.values[a].dtype == c.values[b].dtype);
+    };
+    if (hq.f0 != hk.f0 || hq.i0 != hk.i0 || D / hq.i0 != 128 || hq.in[2] != hk.in[2] || hq.in[3] != hk.in[3] ||
+        !same_dtype(hq.in[1], hk.in[1]) || hq.lane != L.lane || hk.lane != L.lane ||
+        c.values[hq.out].dtype != ov.dtype || c.values[hk.out].dtype != ov.dtype)
+      continue;
+    bool tables = true;
+    for (int t : {hq.in[2], hq.in[3]})
+      if (t >= 0 && (c.values[t].v.size[3] != 64 || !is_packed(c.values[t].v) || numel4(c.values[t].v) != rows * 64))
+        tables = false;
+    for (int wq : {hq.in[1], hk.in[1]})
+      if (wq >= 0 && (!is_packed(c.values[wq].v) || numel4(c.values[wq].v) != 128 || c.values[wq].quant)) tables = false;
+    if (!tables) continue;
+    GemmArgs p{};
+    const GValue& xv = c.values[L.in[0]];
+    p.a_dtype = xv.dtype;
+    p.w_dtype = wv.quant ? NDX_I8 : wv.dtype;
+    p.c_dtype = ov.dtype;
+    p.M = (int)rows;
+    p.N = (int)N;
+    p.K = (int)xv.v.size[3];
+    p.batch = (int)(xv.v.size[0] * xv.v.size[1]);
+    p.tile_hint = second_stream_tile(L, p.M);
+    if (!gemm_qk_norm_ok(p, (int)(2 * D))) {
+      // Where the chosen tile's waves do not hold half a head, the 64x128
+      // or the 128x128 tile: the fusion then does not depend on which
+      // stream the projection runs on.
+      for (int hint : {3, 2}) {
+        p.tile_hint = hint;
+        if (gemm_qk_norm_ok(p, (int)(2 * D))) break;
+        p.tile_hint = 0;
+      }
+      if (!p.tile_hint) continue;
+      L.tile_hint = p.tile_hint;
+    }
+    // Views taken of the head norms' outputs (the query chunks of
+    // Models/QwenImage/QwenImageDit.cs:353-373) name those outputs as their
+    // base: they are re-expressed over the projection's buffer, a stride of
+    // 1, D or rows * D (column, row, batch of the packed [.., rows, D]
+    // output) becoming 1, N or rows * N. Any other view keeps the head norms
+    // apart.
+    auto rebase = [&](int hid, int64_t col0, bool apply) {
+      for (int id = 0; id < (int)c.values.size(); id++) {
+        GValue& v = c.values[id];
+        if (id == hid || v.base != hid) continue;
+        View4 nv = v.v;
+        for (int i = 0; i < 4; i++) {
+          const int64_t st = v.v.stride[i];
+          if (v.v.size[i] <= 1) continue;
+          if (st == 1) nv.stride[i] = 1;
+          else if (st == D) nv.stride[i] = N;
+          else if (st == rows * D) nv.stride[i] = rows * N;
+          else return false;
+        }
+        if (apply) {
+          const int64_t o = v.offset, b = o / (rows * D), r = o % (rows * D) / D, col = o % D;
+          v.v = nv;
+          v.offset = col0 + b * rows * N + r * N + col;
+          v.base = lo;
+        }
+      }
+      return true;
+    };
+    if (!rebase(hq.out, 0, false) || !rebase(hk.out, D, false)) continue;
+    rebase(hq.out, 0, true);
+    rebase(hk.out, D, true);
+    L.i0 = EPI_QK_NORM_ROPE;
+    L.f0 = hq.f0;
+    L.in.resize(9, -1);
+    L.in[5] = hq.in[1];
+    L.in[6] = hk.in[1];
+    L.in[7] = hq.in[2];
+    L.in[8] = hq.in[3];
+    for (int h : hnr) {
+      const GValue x = c.values[src[h].in[0]];
+      GValue& hv = c.values[src[h].out];
+      hv.kind = VK_VIEW;
+      hv.base = lo;
+      hv.offset = x.offset;
+      hv.v = x.v;
+      hv.producer = -1;
+    }
+  }
+
   // Reachability from the outputs (through views to their owners).
   std::vector<char> need_node(src.size(), 0);
   std::function<void(int)> mark_value = [&](int id) {
@@ -1653,6 +1799,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     GNode& x = sched[i];
     GNode& y = sched[i + 1];
     if (x.op != OP_LINEAR || y.op != OP_LINEAR || x.i5 || y.i5 || x.lane != y.lane) continue;
+    if (x.i0 == EPI_QK_NORM_ROPE || y.i0 == EPI_QK_NORM_ROPE) continue;
     const GValue& wx = c.values[x.in[1]];
     const GValue& wy = c.values[y.in[1]];
     const GValue& ax = c.values[x.in[0]];
@@ -1818,6 +1965,9 @@ struct Runner {
       case VK_CONST: return (char*)b.data->ptr;
       default:
         if (m->out_slot[base] >= 0) return (char*)out_ptr[m->out_slot[base]];
+        // Only an owner the planner placed has bytes: anything else is a
+        // compiler error, refused here rather than read from the device.
+        if (b.base != base || m->arena_off[base] < 0) fail(NDX_INVALID_STATE, "a value with no storage was read");
         return arena + m->arena_off[base];
     }
   }
@@ -1859,7 +2009,7 @@ struct Runner {
       a.w_dtype = w.dtype;
     }
     a.batch_w = 0;
-    a.tile_hint = second_stream_tile(n, a.M);
+    a.tile_hint = n.tile_hint ? n.tile_hint : second_stream_tile(n, a.M);
     a.c = ptr(n.out);
     // A SwiGLU writes one column per interleaved (gate, up) pair: N / 2.
     a.ldc = n.i0 == EPI_SWIGLU ? a.N / 2 : a.N;
@@ -1889,6 +2039,19 @@ struct Runner {
       a.ldr = ld;
       a.batch_r = bs;
       a.r_dtype = r.dtype;
+    }
+    if (n.i0 == EPI_QK_NORM_ROPE) {
+      a.qk_cols = 2 * (a.N / 3);
+      a.norm_eps = n.f0;
+      if (n.in[5] >= 0) {
+        a.norm_q = ptr(n.in[5]);
+        a.norm_k = ptr(n.in[6]);
+        a.norm_dtype = val(n.in[5]).dtype;
+      }
+      if (n.in[7] >= 0) {
+        a.rope_cos = (const float*)ptr(n.in[7]);
+        a.rope_sin = (const float*)ptr(n.in[8]);
+      }
     }
     return a;
   }
@@ -2358,7 +2521,8 @@ void compute_families(ndx_model* m) {
     p.N = (int)w.v.size[2];
     p.K = (int)x.v.size[3];
     p.batch = (int)(x.v.size[0] * x.v.size[1]);
-    p.tile_hint = second_stream_tile(k, p.M);
+    p.tile_hint = k.tile_hint ? k.tile_hint : second_stream_tile(k, p.M);
+    p.c_dtype = m->values[k.out].dtype;
     return p;
   };
   // NDX_PROFILE_LANES=1 names the second stream's kernels apart ("@lane1"),

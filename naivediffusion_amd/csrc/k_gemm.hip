@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <stdexcept>
 
 #include "k_common.h"
 
@@ -277,15 +278,143 @@ __device__ __forceinline__ void epilogue_slices(const GemmArgs& a, int64_t bidx,
   }
 }
 
+// EPI_QK_NORM_ROPE for one 32-row slice of a wave of 64 columns: half a
+// head of 128, the other half in the partner wave (wave ^ 1, same rows).
+// Each lane walks eight rows of four columns as epilogue_slice does. The
+// product plus bias is rounded to the output type (the projection's
+// output), each row's sum of squares over the wave's 64 columns meets the
+// partner's in LDS (ssq), the normalised, scaled values are rounded (the
+// head norm's output) and staged, and after a barrier each lane reads the
+// partner's value of the same rotary frequency: the low half stores
+// l cos - h sin, the high half h cos + l sin (Transformer.cs:37-64).
+// ssq holds 32 floats per wave.
+__device__ __forceinline__ void qk_norm_rope_slice(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[2], float* stage,
+                                                   const float* partner_stage, float* ssq, int row0, int col0) {
+  constexpr int CS = 64 + 4, C4 = 16, RSTEP = 4, IT = 8;
+  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
+  const int wave = threadIdx.x >> 6;
+  const int c4 = lane % C4, rl0 = lane / C4;
+  const int col = col0 + c4 * 4;
+  const int dim = col & 127;  // within the head
+  const bool high = dim >= 64;
+  // The weight of the wave's third (q or k), picked by arithmetic: a select
+  // between two fields of the argument block would copy the block to
+  // scratch memory.
+  const uintptr_t wq = (uintptr_t)a.norm_q, wk = (uintptr_t)a.norm_k;
+  const void* nw = (const void*)(wq + uintptr_t(col0 >= a.qk_cols / 2) * (wk - wq));
+  float bias[4], w[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    bias[e] = a.bias ? load_f(a.bias, a.bias_dtype, col + e) : 0.f;
+    w[e] = nw ? load_f(nw, a.norm_dtype, dim + e) : 1.f;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[j][r];
+  __syncthreads();
+  // The product rounded to the output type, back into the stage; each row's
+  // sum of squares over the wave's 64 columns into ssq.
+#pragma unroll
+  for (int t = 0; t < IT; t++) {
+    const int rl = rl0 + t * RSTEP;
+    float4* sp = (float4*)&stage[rl * CS + c4 * 4];
+    const float4 s = *sp;
+    const float v0 = round_to(s.x + bias[0], a.c_dtype), v1 = round_to(s.y + bias[1], a.c_dtype),
+                v2 = round_to(s.z + bias[2], a.c_dtype), v3 = round_to(s.w + bias[3], a.c_dtype);
+    *sp = make_float4(v0, v1, v2, v3);
+    float ss = v0 * v0 + v1 * v1 + v2 * v2 + v3 * v3;
+#pragma unroll
+    for (int o = 1; o < C4; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    if (c4 == 0) ssq[wave * 32 + rl] = ss;
+  }
+  __syncthreads();
+  // The rotary table rows of this lane's eight rows are requested here, so
+  // their latency passes under this pass and its barrier (rows past M read
+  // row M - 1).
+  const float* __restrict__ cos_t = a.rope_cos;
+  const float* __restrict__ sin_t = a.rope_sin;
+  float4 cs[IT], sn[IT];
+  if (cos_t) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) {
+      const int64_t row = min(row0 + rl0 + t * RSTEP, a.M - 1);
+      cs[t] = *(const float4*)(cos_t + row * 64 + (dim & 63));
+      sn[t] = *(const float4*)(sin_t + row * 64 + (dim & 63));
+    }
+  }
+  // The head norm's output, rounded, back into the stage.
+  const float* pssq = ssq + (wave ^ 1) * 32;
+#pragma unroll
+  for (int t = 0; t < IT; t++) {
+    const int rl = rl0 + t * RSTEP;
+    const float r = 1.0f / sqrtf((ssq[wave * 32 + rl] + pssq[rl]) * (1.0f / 128) + a.norm_eps);
+    float4* sp = (float4*)&stage[rl * CS + c4 * 4];
+    const float4 v = *sp;
+    *sp = make_float4(round_to(v.x * r * w[0], a.c_dtype), round_to(v.y * r * w[1], a.c_dtype),
+                      round_to(v.z * r * w[2], a.c_dtype), round_to(v.w * r * w[3], a.c_dtype));
+  }
+  __syncthreads();
+  const bool out_vec = aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype));
+#pragma unroll
+  for (int t = 0; t < IT; t++) {
+    const int rl = rl0 + t * RSTEP, row = row0 + rl;
+    if (row >= a.M) continue;
+    const float4 n = *(const float4*)&stage[rl * CS + c4 * 4];
+    float y[4] = {n.x, n.y, n.z, n.w};
+    if (cos_t) {
+      const float4 p = *(const float4*)&partner_stage[rl * CS + c4 * 4];
+      const float nn[4] = {n.x, n.y, n.z, n.w}, pp[4] = {p.x, p.y, p.z, p.w};
+      const float cc[4] = {cs[t].x, cs[t].y, cs[t].z, cs[t].w}, sv[4] = {sn[t].x, sn[t].y, sn[t].z, sn[t].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[e] = high ? nn[e] * cc[e] + pp[e] * sv[e] : nn[e] * cc[e] - pp[e] * sv[e];
+    }
+    const int64_t co = bidx * a.batch_c + int64_t(row) * a.ldc + col;
+    if (out_vec) {
+      store4_vec(a.c, a.c_dtype, co, y);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) store_f(a.c, a.c_dtype, co + e, y[e]);
+    }
+  }
+  __syncthreads();
+}
+
+// Slices I .. TM - 1 of EPI_QK_NORM_ROPE, expanded at compile time as
+// epilogue_slices is.
+template <int I, int TM>
+__device__ __forceinline__ void qk_norm_rope_slices(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][2],
+                                                    float* stage, const float* partner_stage, float* ssq, int row0,
+                                                    int col0) {
+  if constexpr (I < TM) {
+    qk_norm_rope_slice(a, bidx, acc[I], stage, partner_stage, ssq, row0 + I * 32, col0);
+    qk_norm_rope_slices<I + 1, TM>(a, bidx, acc, stage, partner_stage, ssq, row0, col0);
+  }
+}
+
 // Writes the accumulators of one wave (TM x TN tiles of 32 x 32, the MFMA
 // layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4)
 // through the epilogue, one 32-row slice at a time. A lane's four columns
 // are the same in every row it visits, so its bias and gate are read once.
 // stage must hold 32 x (WN + 4) floats for each wave and be free (the main
-// loop is done).
-template <int TM, int TN, int WN>
+// loop is done). QKN: the kernel takes EPI_QK_NORM_ROPE (stage then holds
+// 32 more floats per wave after the waves' stages); only its own
+// instantiations carry that code.
+template <int TM, int TN, int WN, bool QKN = false>
 __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][TN],
                                                 float* stage, int row0, int col0) {
+  if constexpr (QKN && WN == 64) {
+    // The whole workgroup takes this path or none: qk_cols is a multiple of
+    // the tile's width (gemm_qk_norm_ok).
+    if (a.epilogue == EPI_QK_NORM_ROPE && col0 < a.qk_cols) {
+      constexpr int CS = WN + 4;
+      const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+      float* all = stage - wave * 32 * CS;
+      float* ssq = all + waves * 32 * CS;
+      qk_norm_rope_slices<0, TM>(a, bidx, acc, stage, all + (wave ^ 1) * 32 * CS, ssq, row0, col0);
+      return;
+    }
+  }
   constexpr int C4 = WN / 4;
   const int lane = threadIdx.x & 63;
   EpiLane L;
@@ -483,7 +612,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
 // a0 and a1 are two products with the same N, K and batch run as one grid
 // (a0's row tiles first, then a1's); a1.M = 0 for a single product.
-template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL>
+template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
                                                                                     int grid) {
   typedef typename MfmaOp<T>::V V;
@@ -494,7 +623,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   constexpr int B_LOADS = BN / 8 / NW;
   static_assert(A_LOADS * 8 * NW == BM && B_LOADS * 8 * NW == BN, "tile rows do not split over the waves");
   constexpr int TILE_BYTES = 2 * (BM + BN) * BK * (int)sizeof(T);
-  constexpr int STAGE_BYTES = NW * 32 * (WN + 4) * 4;
+  // The epilogue's stage, and for EPI_QK_NORM_ROPE 32 floats per wave after
+  // it (the row sums).
+  constexpr int STAGE_BYTES = NW * 32 * (WN + 4) * 4 + (QKN ? NW * 32 * 4 : 0);
   __shared__ __attribute__((aligned(1024))) char smem[TILE_BYTES > STAGE_BYTES ? TILE_BYTES : STAGE_BYTES];
   T (*As)[BM * BK] = reinterpret_cast<T (*)[BM * BK]>(smem);
   T (*Bs)[BN * BK] = reinterpret_cast<T (*)[BN * BK]>(smem + 2 * BM * BK * sizeof(T));
@@ -685,7 +816,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   __syncthreads();
 
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
-  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  staged_epilogue<TM, TN, WN, QKN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ---- int8 weights, direct to LDS ----------------------------------------------
@@ -1442,6 +1573,17 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
       hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, true, true>), g, b, 0, s, a, a1, grid);
   } else {
     const bool kfull = a.K % BK == 0;
+    if constexpr (WN == 64) {
+      // The fused head norm (whole K tiles only, one problem per launch).
+      if (a.epilogue == EPI_QK_NORM_ROPE) {
+        if (a.a_dtype == NDX_BF16)
+          hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true, true>), g, b, 0, s, a, a1, grid);
+        else
+          hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true, true>), g, b, 0, s, a, a1,
+                             grid);
+        return;
+      }
+    }
     if (a.a_dtype == NDX_BF16) {
       if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true>), g, b, 0, s, a, a1, grid);
       else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, false>), g, b, 0, s, a, a1, grid);
@@ -1550,6 +1692,7 @@ bool gemm_pair_pays(int64_t M1, int64_t M2, int64_t N, int64_t K, int64_t batch)
 }
 
 bool launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t s) {
+  if (a.epilogue == EPI_QK_NORM_ROPE || b.epilogue == EPI_QK_NORM_ROPE) return false;
   if (a.M == 0 || b.M == 0 || a.N != b.N || a.K != b.K || a.batch != b.batch || a.a_dtype != b.a_dtype ||
       a.w_dtype != b.w_dtype || !is_lds_kind(choose(a)) || !is_lds_kind(choose(b)))
     return false;
@@ -1573,8 +1716,22 @@ const char* gemm_pair_family(const GemmArgs& a, const GemmArgs& b) {
   return gemm_family(both);
 }
 
+bool gemm_qk_norm_ok(const GemmArgs& a, int qk_cols) {
+  if (qk_cols <= 0 || qk_cols % 128 || a.K % BK ||
+      (a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16 && a.c_dtype != NDX_F32))
+    return false;
+  switch (choose(a)) {
+    case K_LDS_256W8: return qk_cols % 256 == 0;
+    case K_LDS_128:
+    case K_LDS_64x128: return true;
+    default: return false;
+  }
+}
+
 void launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M == 0 || a.N == 0 || a.batch == 0) return;
+  if (a.epilogue == EPI_QK_NORM_ROPE && !gemm_qk_norm_ok(a, a.qk_cols))
+    throw std::runtime_error("gemm: the fused head norm needs a 64-column-wave tile dividing the q and k columns");
   switch (choose(a)) {
     case K_GEMV: {
       dim3 g((a.N + 15) / 16, a.batch);

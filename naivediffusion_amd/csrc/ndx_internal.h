@@ -78,6 +78,10 @@ enum Epilogue {
   EPI_GATED_RESIDUAL = NDX_EPI_GATED_RESIDUAL,
   EPI_RESIDUAL = NDX_EPI_RESIDUAL,
   EPI_SWIGLU = NDX_EPI_SWIGLU,
+  // Compile-time only (no public code): a QKV projection whose q and k
+  // thirds go through the per-head RMSNorm and rotary embedding in the
+  // epilogue (the fields norm_* and rope_* of GemmArgs).
+  EPI_QK_NORM_ROPE = 100,
 };
 
 // One linear layer's product: C[b] = epi(A[b] (M x K, rows lda apart) *
@@ -110,6 +114,15 @@ struct GemmArgs {
   // The 16-bit tile to use regardless of the latency model (0: the model;
   // 1..4: 256x256, 128x128, 64x128, 64x64).
   int tile_hint;
+  // EPI_QK_NORM_ROPE: columns below qk_cols are q (the first half) and k
+  // heads of 128. Each head of a row is RMS-normalised (norm_eps) over the
+  // product rounded to c_dtype, scaled by norm_q / norm_k (null: none),
+  // rounded, then rotated (rotate-half) in fp32 by rope_cos / rope_sin
+  // ([M, 64] fp32 rows, the row's position within its batch; null: no
+  // rotation) and stored; columns from qk_cols on get the bias only.
+  const void* norm_q; const void* norm_k; int norm_dtype;
+  const float* rope_cos; const float* rope_sin;
+  int qk_cols; float norm_eps;
 };
 
 // DmlOps.Gemm in full generality (any strides, transposes, alpha, beta): a
@@ -271,6 +284,10 @@ void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
                            hipStream_t s, int64_t cin_pad = 0);
 const char* conv_family(const ConvArgs& a);
+// Whether the kernel launch_gemm picks for a (pointers aside) can run
+// EPI_QK_NORM_ROPE with qk_cols: a 16-bit direct-to-LDS tile of 64-column
+// waves whose width divides qk_cols.
+bool gemm_qk_norm_ok(const GemmArgs& a, int qk_cols);
 void launch_elementwise(const ElemArgs& a, hipStream_t s);
 void launch_upsample(const UpsampleArgs& a, hipStream_t s);
 void launch_patch(const PatchArgs& a, hipStream_t s);

@@ -360,6 +360,54 @@ def test_head_norm_rotate_against_oracle(device, dtype):
     assert rel_err(o2.reshape(T, -1), ref) <= tol
 
 
+@pytest.mark.parametrize("tile,fused", [("256w8lds", True), ("128lds", True), ("64x128lds", True), ("64x64lds", False)])
+def test_qkv_projection_with_fused_head_norm(device, monkeypatch, tile, fused):
+    """With NDX_FUSE_QK_NORM=1, Rotate(HeadNorm(...)) of a QKV projection's
+    q and k thirds (QwenImageDit.cs:342-347) runs in the projection's
+    epilogue on the tiles whose waves hold half a head (no head-norm kernel
+    runs), and stays a pass of its own on a tile whose waves do not; 300
+    rows leave a partial tile.
+    Both against the oracle: the product rounded to bf16, the RMS norm over
+    each head of 128 with the weight, the rotation; v is the rounded
+    product's last third."""
+    print(f"[gpu] fused qkv head norm, tile {tile}", flush=True)
+    monkeypatch.setenv("NDX_GEMM_TILE", tile)
+    monkeypatch.setenv("NDX_FUSE_QK_NORM", "1")
+    T, Dm, H, d = 300, 256, 4, 128
+    D = H * d
+    x = bf(normal("fq_x", (1, 1, T, Dm)))
+    w = bf(normal("fq_w", (3 * D, Dm), 1.0 / math.sqrt(Dm)))
+    b = bf(normal("fq_b", (3 * D,), 0.1))
+    wq, wk = bf(normal("fq_q", (d,), 0.2) + 1), bf(normal("fq_k", (d,), 0.2) + 1)
+    cos, sin = oracle.mmdit_rope_tables(10, 30, 0)
+    dt = DT.BFloat16
+    model = nd.ModelBuilder(device, dt)
+    xi = model.Placeholder([1, 1, T, Dm], dt)
+    ci = model.Placeholder([1, T, 1, 64], DT.Float32)
+    si = model.Placeholder([1, T, 1, 64], DT.Float32)
+    qkv = Layers.Linear(model, xi, HostTensor.FromFloats(w), HostTensor.FromFloats(b))
+    q = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, 0], [1, 1, T, D]), HostTensor.FromFloats(wq), H,
+                                   1e-6, ci, si, dt)
+    k = Transformer.HeadNormRotate(model, Ops.Slice(qkv, [0, 0, 0, D], [1, 1, T, D]), HostTensor.FromFloats(wk), H,
+                                   1e-6, ci, si, dt)
+    v = Ops.ActivationIdentity(Ops.Slice(qkv, [0, 0, 0, 2 * D], [1, 1, T, D]))
+    model.Compile([q, k, v])
+    model.Compiled.SetProfiling(True)
+    oq, ok_, ov = run(model, HostTensor.FromFloats(x).ConvertTo(dt), HostTensor.FromFloats(cos.reshape(1, T, 1, 64)),
+                      HostTensor.FromFloats(sin.reshape(1, T, 1, 64)))
+    families = set(model.Compiled.Profile())
+    model.Dispose()
+    p = bf(oracle.linear(x.reshape(T, Dm), w, b))
+    want = [oracle.rope(oracle.rms_norm(p[:, i * D:(i + 1) * D].reshape(T * H, d), wn, 1e-6).reshape(T, D), H, cos,
+                        sin) for i, wn in ((0, wq), (1, wk))]
+    for got, ref in zip((oq, ok_), want):
+        err = rel_err(got.reshape(T, D), ref)
+        print(f"[gpu]   rel err {err:.2e} via {sorted(families)}", flush=True)
+        assert err <= BF16_TOL
+    assert rel_err(ov.reshape(T, D), p[:, 2 * D:]) <= BF16_TOL
+    assert ("head_norm_rotate" not in families) == fused, families
+
+
 # ---- the reference's smoke cases (Cli/SmokeTest.cs) ---------------------------------------
 
 def test_smoke_gemm_and_broadcast_weight(device):

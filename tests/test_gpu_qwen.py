@@ -70,11 +70,16 @@ def device_copy(device, w):
     return {k: device.Upload(HostTensor.FromFloats(v).ConvertTo(DT.BFloat16)) for k, v in w.items()}
 
 
-@pytest.mark.parametrize("compute,tol", [(DT.BFloat16, 2e-2), (DT.Float32, 1e-3)])
-def test_qwen_block_at_model_width(device, full_block, compute, tol):
+@pytest.mark.parametrize("compute,tol,fuse", [(DT.BFloat16, 2e-2, "0"), (DT.Float32, 1e-3, "0"),
+                                              (DT.BFloat16, 2e-2, "1")])
+def test_qwen_block_at_model_width(device, full_block, compute, tol, fuse, monkeypatch):
+    """The block against the oracle; with NDX_FUSE_QK_NORM=1 the head norms
+    run in the QKV projection's epilogue and the attention reads query
+    chunks of the projection's rows (views re-expressed over its buffer)."""
+    monkeypatch.setenv("NDX_FUSE_QK_NORM", fuse)
     w, x, time, cond, ref, n_img, n_txt = full_block
     N = n_img + n_txt
-    say(f"qwen block {compute.name}")
+    say(f"qwen block {compute.name} fused head norm {fuse}")
     model = qwen.build_block_model(device, FULL, device_copy(device, w), n_img, n_txt, compute)
     out = model.Run(HostTensor.FromFloats(x.reshape(1, 1, N, -1)), HostTensor.FromFloats(time.reshape(1, 1, 2, -1)),
                     HostTensor.FromInt32(cond["text_mask"], 1, 1, n_txt, n_txt),
