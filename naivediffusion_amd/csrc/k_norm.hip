@@ -487,7 +487,8 @@ __global__ __launch_bounds__(THREADS) void channel_norm_vec_kernel(ChannelNormAr
   constexpr int WAVES = THREADS / 64, ROWS = THREADS / 8, PER_PX = ROWS / 8;
   __shared__ float red[2][WAVES][64];
   __shared__ float stat[2][64];
-  __shared__ __align__(16) uint16_t tile[ROWS][66];
+  // RPT > 0: the whole block [channel][pixel]; else one ROWS-channel slab.
+  __shared__ __align__(16) uint16_t tile[RPT > 0 ? RPT * ROWS : ROWS][66];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = t & 7, row = t >> 3;
   const int64_t C = a.C, P = a.P;
   const int64_t n = blockIdx.y, p0 = int64_t(blockIdx.x) * 64;
@@ -599,9 +600,37 @@ __global__ __launch_bounds__(THREADS) void channel_norm_vec_kernel(ChannelNormAr
     __syncthreads();
   };
   if constexpr (RPT > 0) {
+    // The block's rows into LDS at once, then its 64 pixels x C outputs,
+    // one contiguous run of the tokens, written in 16-byte pieces: every
+    // cache line whole, one barrier. The weight and bias go to LDS as fp32
+    // first (each output piece reads eight of them).
+    __shared__ float wb[2][RPT * ROWS];
+    for (int c = t; c < C; c += THREADS) {
+      wb[0][c] = a.weight ? load_f(a.weight, a.w_dtype, c) : 1.f;
+      wb[1][c] = a.bias ? load_f(a.bias, a.b_dtype, c) : 0.f;
+    }
 #pragma unroll
-    for (int r = 0; r < RPT; r++)
-      if (ROWS * r < C) slab(ROWS * r, keep[r]);
+    for (int r = 0; r < RPT; r++) {
+      uint32_t* d = (uint32_t*)&tile[row + ROWS * r][8 * g];
+      d[0] = keep[r].x;
+      d[1] = keep[r].y;
+      d[2] = keep[r].z;
+      d[3] = keep[r].w;
+    }
+    __syncthreads();
+    const int64_t pieces = min(int64_t(64), P - p0) * C / 8;
+    for (int64_t i = t; i < pieces; i += THREADS) {
+      const int px = (int)(i * 8 / C), c = (int)(i * 8 - int64_t(px) * C);
+      const float mean = stat[0][px], rstd = stat[1][px];
+      __align__(16) T out[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float v = (half_to_f<T>(tile[c + e][px]) - mean) * rstd * wb[0][c + e] + wb[1][c + e];
+        if (a.silu) v = silu_f((float)(T)v);
+        out[e] = (T)v;
+      }
+      *(uint4*)(y + i * 8) = *(const uint4*)out;
+    }
   } else {
     for (int64_t c0 = 0; c0 < C; c0 += ROWS) slab(c0, load_row(c0 + row));
   }
