@@ -247,7 +247,35 @@ __global__ void upsample_kernel(UpsampleArgs a, int64_t total) {
   }
 }
 
+// The 2x case for 16-bit images whose rows are read four pixels (8 bytes)
+// at a time: each thread writes the 2x8 output pixels of four input pixels
+// as two 16-byte stores.
+__global__ void upsample2_vec_kernel(UpsampleArgs a, int64_t total) {
+  const int64_t wq = a.W / 4, Wo = a.W * 2, Ho = a.H * 2;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    int64_t r = i;
+    const int64_t xq = r % wq;
+    r /= wq;
+    const int64_t y = r % a.H;
+    r /= a.H;
+    const int64_t c = r % a.C, n = r / a.C;
+    const uint2 u = *(const uint2*)((const uint16_t*)a.x + offset_of(a.vx, n, c, y, xq * 4));
+    const uint4 o = make_uint4((u.x & 0xffffu) | (u.x << 16), (u.x >> 16) | (u.x & 0xffff0000u),
+                               (u.y & 0xffffu) | (u.y << 16), (u.y >> 16) | (u.y & 0xffff0000u));
+    uint16_t* dst = (uint16_t*)a.y + ((n * a.C + c) * Ho + 2 * y) * Wo + 8 * xq;
+    *(uint4*)dst = o;
+    *(uint4*)(dst + Wo) = o;
+  }
+}
+
 void launch_upsample(const UpsampleArgs& a, hipStream_t s) {
+  const View4& v = a.vx;
+  if (a.scale == 2 && dtype_size(a.dtype) == 2 && a.W % 4 == 0 && v.stride[3] == 1 && v.stride[2] % 4 == 0 &&
+      v.stride[1] % 4 == 0 && v.stride[0] % 4 == 0 && (uintptr_t)a.x % 8 == 0 && (uintptr_t)a.y % 16 == 0) {
+    const int64_t total = a.N * a.C * a.H * (a.W / 4);
+    hipLaunchKernelGGL(upsample2_vec_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
+    return;
+  }
   int64_t total = a.N * a.C * a.H * a.scale * a.W * a.scale;
   hipLaunchKernelGGL(upsample_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a, total);
 }

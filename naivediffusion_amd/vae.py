@@ -504,9 +504,12 @@ def build_wan22_decoder(device: Device, cfg: Wan22Config, weights: dict, height:
             h = wan_residual_block(model, W, h, f"{p}.{index}")
             index += 1
         if level != levels - 1:
-            h = Layers.Conv2d(model, Layers.UpsampleNearest(h), W(f"{p}.{index}.resample.1.weight"),
-                              v(f"{p}.{index}.resample.1.bias"))
-            h = h + up_shortcut(level_in, h.Shape[1], WAN22_TEMPORAL[levels - 2 - level])
+            # The up-shortcut's sum rides the resample convolution's residual
+            # epilogue (the product rounded first, as the separate add has it).
+            wr = W(f"{p}.{index}.resample.1.weight")
+            shortcut = up_shortcut(level_in, wr.Shape[0], WAN22_TEMPORAL[levels - 2 - level])
+            h = Layers.Conv2d(model, Layers.UpsampleNearest(h), wr, v(f"{p}.{index}.resample.1.bias"),
+                              residual=shortcut)
     _, c, hh, ww = h.Shape
     t = Layers.Silu(_channel_rms_tokens(model, W, h, "decoder.head.0.gamma"))
     image = Layers.Conv2d(model, Layers.ToImage(t, hh, ww), W("decoder.head.2.weight"), v("decoder.head.2.bias"))

@@ -408,6 +408,28 @@ def test_qkv_projection_with_fused_head_norm(device, monkeypatch, tile, fused):
     assert ("head_norm_rotate" not in families) == fused, families
 
 
+@pytest.mark.parametrize("dtype", [DT.BFloat16, DT.Float16, DT.Float32])
+@pytest.mark.parametrize("shape,odd", [((2, 6, 5, 8), False), ((1, 12, 4, 12), True), ((1, 3, 3, 7), False)])
+def test_nearest_upsample_exact(device, dtype, shape, odd):
+    """UpsampleNearest of an image, or of its odd channels (a strided view,
+    as Wan's DupUp3D shortcut takes them), equals numpy's repeat bit for bit:
+    16-bit rows a multiple of 4 wide take the 16-byte kernel, the rest the
+    per-element one."""
+    B, C, H, W = shape
+    print(f"[gpu] upsample {dtype.name} {shape} odd={odd}", flush=True)
+    x = _round(normal("up_x", shape), dtype)
+    g = nd.Graph(device)
+    xi = g.Input(dtype, list(shape))
+    src = Ops.Slice(xi, [0, 1, 0, 0], [B, C - 1, H, W], [1, 2, 1, 1]) if odd else xi
+    m = nd.CompiledModel(g, [Layers.UpsampleNearest(src)], device)
+    host = HostTensor.FromFloats(x)
+    (y,) = m.Dispatch([host if dtype == DT.Float32 else host.ConvertTo(dtype)])
+    m.Dispose()
+    want = x[:, 1::2] if odd else x
+    want = np.repeat(np.repeat(want, 2, 2), 2, 3)
+    np.testing.assert_array_equal(y.ToFloats().reshape(want.shape), want)
+
+
 # ---- the reference's smoke cases (Cli/SmokeTest.cs) ---------------------------------------
 
 def test_smoke_gemm_and_broadcast_weight(device):
