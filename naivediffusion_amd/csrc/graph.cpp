@@ -1106,29 +1106,31 @@ struct Compiler {
   }
 
   // The filter value `wid` (a packed constant [Cout, Cin, kh, kw]) reordered
-  // to [Cout, kh, kw, cin_pad] on the device, as a new constant value, the
-  // channels past Cin zero.
+  // on the device to rows of [kh, kw, cin_pad] (conv_filter_row elements,
+  // the channels past Cin and the row's tail zero), as a new constant value.
   int reordered_filter(int wid, int64_t cin_pad) {
     const GValue& w = values[wid];
     ndx_tensor* src = w.data;
     ndx_tensor* r;
+    const int64_t taps = w.v.size[2] * w.v.size[3], row = conv_filter_row(cin_pad, taps);
+    // [Cout, row] as 4-D: [Cout, cin_pad, kh, kw] when the taps are whole K
+    // tiles, [Cout, row, 1, 1] when K runs over the taps unpadded.
+    const int64_t shape[4] = {w.v.size[0], row == taps * cin_pad ? cin_pad : row,
+                              row == taps * cin_pad ? w.v.size[2] : 1, row == taps * cin_pad ? w.v.size[3] : 1};
     auto it = g->consts->nhwc_filters.find(src);
     if (it != g->consts->nhwc_filters.end()) {
       r = it->second;
     } else {
-      const int64_t shape[4] = {w.v.size[0], cin_pad, w.v.size[2], w.v.size[3]};
       r = new_tensor(g->dev, w.dtype, shape, 4);
       g->consts->tensors.push_back(r);
       g->consts->nhwc_filters[src] = r;
-      launch_reorder_filter(src->ptr, r->ptr, w.dtype, w.v.size[0], w.v.size[1], w.v.size[2] * w.v.size[3],
-                            g->dev->stream, cin_pad);
+      launch_reorder_filter(src->ptr, r->ptr, w.dtype, w.v.size[0], w.v.size[1], taps, g->dev->stream, cin_pad, row);
       hip_check(hipGetLastError(), "filter reorder launch");
       hip_check(hipStreamSynchronize(g->dev->stream), "filter reorder");
     }
     GValue v = w;
     v.data = r;
-    v.v.size[1] = cin_pad;
-    v.v = packed4(v.v.size);
+    v.v = packed4(shape);
     values.push_back(v);
     int id = (int)values.size() - 1;
     values[id].base = id;
@@ -1451,7 +1453,8 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     if (w.quant || w.kind != VK_CONST || w.base != n.in[1] || w.offset != 0 || !w.data) return 0;
     const int64_t cin = conv_gemm_cin(x.dtype, w.dtype, x.v.size[1]);
     const int64_t lim = int64_t(1) << 31;
-    if (!cin || x.v.size[1] * x.v.size[2] * x.v.size[3] * 2 >= lim || numel4(w.v) / x.v.size[1] * cin * 2 >= lim)
+    if (!cin || x.v.size[1] * x.v.size[2] * x.v.size[3] * 2 >= lim ||
+        w.v.size[0] * conv_filter_row(cin, w.v.size[2] * w.v.size[3]) * 2 >= lim)
       return 0;
     return cin;
   };

@@ -113,25 +113,27 @@ void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c
   hipLaunchKernelGGL(nchw_to_nhwc_kernel, g, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, c, hw);
 }
 
-// Filters [cout, cin, taps] -> [cout, taps, cin_pad] (16-bit elements),
-// channels past cin zero.
+// Filters [cout, cin, taps] -> rows of `row` elements holding [taps,
+// cin_pad] (16-bit elements), channels past cin and the row's tail zero.
 __global__ void reorder_filter_kernel(const uint16_t* w, uint16_t* y, int64_t cout, int64_t cin, int64_t taps,
-                                      int64_t cin_pad) {
-  const int64_t total = cout * cin_pad * taps;
+                                      int64_t cin_pad, int64_t row) {
+  const int64_t total = cout * row;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t ci = i % cin_pad, t = (i / cin_pad) % taps, co = i / (cin_pad * taps);
-    y[i] = ci < cin ? w[(co * cin + ci) * taps + t] : uint16_t(0);
+    const int64_t k = i % row, co = i / row;
+    const int64_t ci = k % cin_pad, t = k / cin_pad;
+    y[i] = ci < cin && t < taps ? w[(co * cin + ci) * taps + t] : uint16_t(0);
   }
 }
 
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
-                           hipStream_t s, int64_t cin_pad) {
+                           hipStream_t s, int64_t cin_pad, int64_t row) {
   if (dtype_size(dtype) != 2) throw std::runtime_error("reorder_filter: 16-bit elements only");
   if (cin_pad < cin) cin_pad = cin;
-  const int64_t total = cout * cin_pad * taps;
+  if (row < taps * cin_pad) row = taps * cin_pad;
+  const int64_t total = cout * row;
   const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65536);
   hipLaunchKernelGGL(reorder_filter_kernel, dim3(std::max(blocks, 1)), dim3(256), 0, s, (const uint16_t*)w,
-                     (uint16_t*)y, cout, cin, taps, cin_pad);
+                     (uint16_t*)y, cout, cin, taps, cin_pad, row);
 }
 
 void launch_conv2d(const ConvArgs& a, hipStream_t s) {

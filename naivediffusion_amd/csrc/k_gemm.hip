@@ -679,6 +679,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
     }
   }
 
+  // A convolution whose K runs over the taps without padding between them:
+  // each lane's two 8-channel chunks (q) keep their own tap and channel,
+  // set here for tile 0 and advanced by BK as each tile is issued (tiles
+  // are issued in order, 0 to KT).
+  int cky[2] = {0, 0}, ckx[2] = {0, 0}, cci[2] = {0, 0};
+  if constexpr (CONV) {
+    if (a.conv_kcont) {
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        const int k = kchunk_q[q] * 8, tap = k / a.conv_c;
+        cci[q] = k - tap * a.conv_c;
+        cky[q] = tap / a.conv_kw;
+        ckx[q] = tap - cky[q] * a.conv_kw;
+      }
+    }
+  }
+
   // With K a multiple of BK (KFULL) no tile reaches past K except the one
   // loaded after the last (never read): no per-load K check. A row past M
   // keeps kOutOfRange plus any K offset, still past the buffer's end.
@@ -706,6 +723,33 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
       }
     }
     if constexpr (CONV) {
+      if (a.conv_kcont) {
+        // Each chunk at its own tap: past the last tap (cky == conv_kh) it
+        // reads zeros, as it does outside the image.
+        const int up = a.conv_up, row_w = a.conv_w >> up;
+#pragma unroll
+        for (int i = 0; i < B_LOADS; i++) {
+          const int q = (wave * B_LOADS + i) & 1;
+          const int iy = pix_y[i] + cky[q], ix = pix_x[i] + ckx[q];
+          const bool in = cky[q] < a.conv_kh && (unsigned)iy < (unsigned)a.conv_h && (unsigned)ix < (unsigned)a.conv_w;
+          const uint32_t off =
+              in ? uint32_t((((iy >> up) * row_w + (ix >> up)) * a.conv_c + cci[q]) * ES) : kOutOfRange;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)&Bs[buf][(wave * B_LOADS + i) * 8 * BK], 16, off, 0, 0,
+                                                   0);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          cci[q] += BK;
+          while (cci[q] >= a.conv_c) {
+            cci[q] -= a.conv_c;
+            if (++ckx[q] == a.conv_kw) {
+              ckx[q] = 0;
+              cky[q]++;
+            }
+          }
+        }
+        return;
+      }
       // A K tile lies within one tap (conv_cin is a multiple of BK): (ky,
       // kx) and the channel offset are uniform over the workgroup. An
       // 8-channel chunk at or past conv_c (a multiple of 8) reads zeros;
@@ -1602,9 +1646,11 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
 
 int64_t conv_gemm_cin(int x_dtype, int w_dtype, int64_t cin) {
   if (!((x_dtype == NDX_BF16 || x_dtype == NDX_F16) && w_dtype == x_dtype)) return 0;
-  if (cin % BK == 0) return cin;
-  const int64_t pad = (cin + BK - 1) / BK * BK;
-  return cin % 8 == 0 && 2 * pad <= 3 * cin ? pad : 0;
+  return cin % 8 == 0 ? cin : 0;
+}
+
+int64_t conv_filter_row(int64_t cin_k, int64_t taps) {
+  return cin_k % BK == 0 ? taps * cin_k : (taps * cin_k + BK - 1) / BK * BK;
 }
 
 enum ConvKind { CK_256, CK_128, CK_64x128, CK_64x64 };
@@ -1625,7 +1671,8 @@ static ConvKind conv_choose(const GemmArgs& g) {
 static GemmArgs conv_gemm_args(const ConvArgs& c) {
   GemmArgs g{};
   const int taps = c.kh * c.kw;
-  g.a = c.w; g.lda = int64_t(taps) * c.cin_k; g.batch_a = 0; g.a_dtype = c.x_dtype;
+  const int64_t row = conv_filter_row(c.cin_k, taps);
+  g.a = c.w; g.lda = row; g.batch_a = 0; g.a_dtype = c.x_dtype;
   g.w = c.x; g.ldw = 0; g.batch_w = int64_t(c.H >> c.up) * (c.W >> c.up) * c.Cin; g.w_dtype = c.x_dtype;
   g.c = c.y; g.ldc = int64_t(c.Ho) * c.Wo; g.batch_c = int64_t(c.Cout) * c.Ho * c.Wo; g.c_dtype = c.y_dtype;
   g.row_bias = c.bias; g.row_bias_dtype = c.bias_dtype;
@@ -1633,9 +1680,10 @@ static GemmArgs conv_gemm_args(const ConvArgs& c) {
     g.resid = c.resid; g.ldr = g.ldc; g.batch_r = g.batch_c; g.r_dtype = c.y_dtype;
     g.epilogue = EPI_RESIDUAL;
   }
-  g.M = c.Cout; g.N = c.Ho * c.Wo; g.K = taps * c.cin_k; g.batch = c.N;
+  g.M = c.Cout; g.N = c.Ho * c.Wo; g.K = (int)row; g.batch = c.N;
   g.conv_cin = c.cin_k; g.conv_c = c.Cin; g.conv_h = c.H; g.conv_w = c.W; g.conv_wo = c.Wo; g.conv_kw = c.kw;
   g.conv_stride = c.stride; g.conv_pad = c.pad; g.conv_up = c.up;
+  g.conv_kcont = c.cin_k % BK != 0; g.conv_kh = c.kh;
   return g;
 }
 
@@ -1649,8 +1697,8 @@ const char* conv_family(const ConvArgs& c) {
 }
 
 void launch_conv_gemm(const ConvArgs& c, hipStream_t s) {
-  if (c.cin_k % BK || c.cin_k < c.Cin || c.Cin % 8 || (c.up && (c.H % 2 || c.W % 2)))
-    throw std::runtime_error("conv_gemm: channels per tap must be a multiple of 64 covering a multiple of 8");
+  if (c.cin_k < c.Cin || c.Cin % 8 || (c.cin_k % BK && c.cin_k != c.Cin) || (c.up && (c.H % 2 || c.W % 2)))
+    throw std::runtime_error("conv_gemm: a multiple of 8 input channels, per tap either whole K tiles or unpadded");
   const GemmArgs g = conv_gemm_args(c);
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   switch (conv_choose(g)) {

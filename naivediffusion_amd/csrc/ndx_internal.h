@@ -108,9 +108,12 @@ struct GemmArgs {
   // is output pixel n, gathered from an NHWC input [batch, H, W, conv_c] (w,
   // batch_w elements per image) at taps (ky, kx) of a kw-wide filter whose
   // K index is (ky * kw + kx) * conv_cin + ci; channels ci at or past conv_c
-  // read as zero. With conv_up the input is read through a nearest 2x
-  // upsample: conv_h x conv_w is the upsampled size, memory holds half.
+  // read as zero. With conv_kcont, K runs over the taps with no padding
+  // between them, (ky * kw + kx) * conv_c + ci, past conv_kh * kw taps
+  // zeros. With conv_up the input is read through a nearest 2x upsample:
+  // conv_h x conv_w is the upsampled size, memory holds half.
   int conv_cin, conv_c, conv_h, conv_w, conv_wo, conv_kw, conv_stride, conv_pad, conv_up;
+  int conv_kcont, conv_kh;
   // The 16-bit tile to use regardless of the latency model (0: the model;
   // 1..4: 256x256, 128x128, 64x128, 64x64).
   int tile_hint;
@@ -207,9 +210,11 @@ struct ConvArgs {
   const void* resid;           // [N, Cout, Ho, Wo] packed, same dtype as y
   void* y; int y_dtype;
   int N, Cin, H, W, Cout, kh, kw, stride, pad, Ho, Wo;
-  // Implicit GEMM only: the filter's channels per tap (Cin rounded up to a
-  // multiple of 64, zeros past Cin), and whether x is read through a nearest
-  // 2x upsample (H x W the upsampled size; x holds H/2 x W/2 pixels).
+  // Implicit GEMM only: the filter's channels per tap (a multiple of 64, the
+  // taps each whole K tiles; or Cin itself, a multiple of 8 but not of 64:
+  // the filter [Cout, roundup(kh kw Cin, 64)], K running over the taps with
+  // no padding between them), and whether x is read through a nearest 2x
+  // upsample (H x W the upsampled size; x holds H/2 x W/2 pixels).
   int cin_k, up;
 };
 
@@ -273,16 +278,19 @@ void launch_conv2d(const ConvArgs& a, hipStream_t s);
 void launch_channel_norm(const ChannelNormArgs& a, hipStream_t s);
 // The implicit-GEMM convolution: filters reordered to [Cout, kh, kw, cin_k]
 // (reorder_filter), the input in NHWC (launch_nchw_to_nhwc), 16-bit types.
-// conv_gemm_cin is the K channel count per tap the GEMM runs with: Cin
-// itself for a multiple of 64, Cin rounded up to one (the filter padded
-// with zero channels, the input's missing channels read as zeros) where
-// that adds at most half and Cin is a multiple of 8, else 0: the direct
-// kernel runs instead.
+// conv_gemm_cin is the channel count per tap of the filter the GEMM runs
+// with (ConvArgs::cin_k): Cin for a multiple of 8 (a multiple of 64: whole
+// K tiles per tap; otherwise K contiguous over the taps), else 0: the
+// direct kernel runs instead.
 int64_t conv_gemm_cin(int x_dtype, int w_dtype, int64_t cin);
+// Elements per row of the reordered filter for cin_k channels per tap.
+int64_t conv_filter_row(int64_t cin_k, int64_t taps);
 void launch_conv_gemm(const ConvArgs& a, hipStream_t s);
 void launch_nchw_to_nhwc(const void* x, void* y, int dtype, int64_t n, int64_t c, int64_t hw, hipStream_t s);
+// Filters [cout, cin, taps] -> rows of `row` elements (0: taps * cin_pad)
+// holding [taps, cin_pad], channels past cin and the row's tail zero.
 void launch_reorder_filter(const void* w, void* y, int dtype, int64_t cout, int64_t cin, int64_t taps,
-                           hipStream_t s, int64_t cin_pad = 0);
+                           hipStream_t s, int64_t cin_pad = 0, int64_t row = 0);
 const char* conv_family(const ConvArgs& a);
 // Whether the kernel launch_gemm picks for a (pointers aside) can run
 // EPI_QK_NORM_ROPE with qk_cols: a 16-bit direct-to-LDS tile of 64-column

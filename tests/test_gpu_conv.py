@@ -4,7 +4,8 @@ cross-correlation: the implicit-GEMM kernel at SDXL's shapes (3x3 pad 1,
 the stride-2 downsampler, the 1x1 shortcut with the resnet's residual add)
 scaled down in extent, ragged extents that leave partial pixel tiles, every
 tile variant pinned, and the direct kernel for what the implicit GEMM does
-not take (4 input channels, int8 filters). Tolerance: max|gpu - oracle| /
+not take (4 input channels, int8 filters). Input channels that are a
+multiple of 8 but not of 64 run with K contiguous over the taps. Tolerance: max|gpu - oracle| /
 max|oracle| <= 1e-2 at fp16, 2e-2 at bf16."""
 
 import numpy as np
@@ -58,11 +59,14 @@ CASES = [
     (2, 640, 8, 8, 1280, 3, 1, 1),
     (1, 192, 9, 31, 96, 3, 1, 1),
     # Channel counts that are multiples of 8 but not of 64 (the Wan VAE's
-    # 144 and 288): the filter padded with zero channels to 192 and 320, the
-    # input's missing channels read as zeros.
+    # 144 and 288, and narrower ones whose taps share a K tile): K runs over
+    # the taps with no padding between them.
     (1, 144, 13, 11, 144, 3, 1, 1),
     (2, 288, 7, 9, 144, 1, 1, 0),
     (1, 288, 10, 6, 576, 3, 2, 1),
+    (1, 16, 9, 11, 64, 3, 1, 1),
+    (2, 40, 8, 6, 96, 3, 2, 1),
+    (1, 8, 12, 12, 32, 3, 1, 1),
 ]
 
 
