@@ -29,7 +29,7 @@ import numpy as np
 from . import rng
 from .graph import ModelBuilder, Ops
 from .layers import Layers
-from .tensors import Device, HostDataType, HostTensor
+from .tensors import Device, DeviceTensor, HostDataType, HostTensor
 from .weights import WeightSet
 
 
@@ -228,10 +228,34 @@ def resnet_block(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, silu_tem
     return Layers.Conv2d(model, h, W(f"{p}.conv2.weight"), v("conv2.bias"), residual=x)
 
 
-def transformer_block(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, context, p: str, heads: int):
+def context_kv(model: ModelBuilder, W: WeightSet, context):
+    """The cross-attention keys and values of the context for every
+    transformer block at once: the context is the same for all of them, so
+    their to_k / to_v projections (UNetLayers.DiffusersAttention, :14-26)
+    stack into one product over the context's rows instead of one small
+    product per block. Returns {block prefix: (k, v)}, views of the result."""
+    blocks = sorted(n[: -len(".attn2.to_k.weight")] for n in W.weights if n.endswith(".attn2.to_k.weight"))
+    if not blocks:
+        return {}
+    names = [f"{b}.attn2.{t}.weight" for b in blocks for t in ("to_k", "to_v")]
+    kv = Layers.Linear(model, context, W.stacked(names))
+    b_, _, nc, _ = kv.Shape
+    out, col = {}, 0
+    for blk in blocks:
+        w = W.weights[f"{blk}.attn2.to_k.weight"]
+        c = w.Shape[0] if isinstance(w, DeviceTensor) else len(w)
+        out[blk] = (Ops.Slice(kv, [0, 0, 0, col], [b_, 1, nc, c]), Ops.Slice(kv, [0, 0, 0, col + c], [b_, 1, nc, c]))
+        col += 2 * c
+    return out
+
+
+def transformer_block(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, context, p: str, heads: int,
+                      kv_all=None):
     """UNetModel.TransformerBlock (:258-276) with UNetLayers.DiffusersAttention
     (:14-26) and Geglu (:30-47): self-attention, cross-attention into the
-    context, the gated feed-forward, each on a LayerNorm of x and added back."""
+    context, the gated feed-forward, each on a LayerNorm of x and added back.
+    kv_all: the context's keys and values made for every block at once
+    (context_kv); without it the block projects the context itself."""
     v = lambda n: W(f"{p}.{n}", "norm")
     b, _, n, c = x.Shape
     eps = cfg.layer_norm_eps
@@ -246,10 +270,13 @@ def transformer_block(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, con
     h = Layers.LayerNorm(model, x, v("norm2.weight"), v("norm2.bias"), eps)
     a = f"{p}.attn2"
     q = Layers.Linear(model, h, W(f"{a}.to_q.weight"))
-    nc = context.Shape[2]
-    kv = Layers.Linear(model, context, W.stacked([f"{a}.to_k.weight", f"{a}.to_v.weight"]))
-    k = Ops.Slice(kv, [0, 0, 0, 0], [b, 1, nc, c])
-    val = Ops.Slice(kv, [0, 0, 0, c], [b, 1, nc, c])
+    if kv_all and p in kv_all:
+        k, val = kv_all[p]
+    else:
+        nc = context.Shape[2]
+        kv = Layers.Linear(model, context, W.stacked([f"{a}.to_k.weight", f"{a}.to_v.weight"]))
+        k = Ops.Slice(kv, [0, 0, 0, 0], [b, 1, nc, c])
+        val = Ops.Slice(kv, [0, 0, 0, c], [b, 1, nc, c])
     x = Layers.Linear(model, Layers.Attend(q, k, val, heads), W(f"{a}.to_out.0.weight"), v("attn2.to_out.0.bias"),
                       residual=x)
 
@@ -261,7 +288,8 @@ def transformer_block(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, con
     return Layers.Linear(model, gated, W(f"{p}.ff.net.2.weight"), v("ff.net.2.bias"), residual=x)
 
 
-def transformer2d(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, context, p: str, heads: int, layers: int):
+def transformer2d(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, context, p: str, heads: int, layers: int,
+                  kv_all=None):
     """UNetModel.Transformer2d (:279-301): GroupNorm, to tokens, proj_in, the
     blocks, proj_out, back to the image, plus the input."""
     _, _, height, width = x.Shape
@@ -269,18 +297,18 @@ def transformer2d(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, context
     normed = Layers.GroupNorm(model, x, v("norm.weight"), v("norm.bias"), cfg.groups, cfg.transformer_eps)
     tokens = Layers.Linear(model, Layers.ToTokens(normed), W(f"{p}.proj_in.weight"), v("proj_in.bias"))
     for j in range(layers):
-        tokens = transformer_block(model, W, cfg, tokens, context, f"{p}.transformer_blocks.{j}", heads)
+        tokens = transformer_block(model, W, cfg, tokens, context, f"{p}.transformer_blocks.{j}", heads, kv_all)
     tokens = Layers.Linear(model, tokens, W(f"{p}.proj_out.weight"), v("proj_out.bias"))
     return Layers.ToImage(tokens, height, width) + x
 
 
 def unit(model: ModelBuilder, W: WeightSet, cfg: SdxlConfig, x, silu_temb, context, prefix: str, index: int,
-         level: int):
+         level: int, kv_all=None):
     """UNetModel.Unit (:306-318): a resnet, then the level's transformers."""
     x = resnet_block(model, W, cfg, x, silu_temb, f"{prefix}.resnets.{index}")
     layers = cfg.transformer_layers[level]
     if layers:
-        x = transformer2d(model, W, cfg, x, context, f"{prefix}.attentions.{index}", cfg.heads[level], layers)
+        x = transformer2d(model, W, cfg, x, context, f"{prefix}.attentions.{index}", cfg.heads[level], layers, kv_all)
     return x
 
 
@@ -298,6 +326,7 @@ def build_unet(device: Device, cfg: SdxlConfig, weights: dict, batch: int, laten
     add = model.Placeholder([batch, 1, 1, cfg.add_width], compute)
     context = model.Placeholder([batch, 1, tokens, cfg.context_width], compute)
 
+    kv_all = context_kv(model, W, context)
     temb = embedding_mlp(model, W, time, "time_embedding") + embedding_mlp(model, W, add, "add_embedding")
     silu_temb = Layers.Silu(temb)
     skips = [Layers.Conv2d(model, sample, W("conv_in.weight"), W("conv_in.bias", "norm"))]
@@ -305,13 +334,14 @@ def build_unet(device: Device, cfg: SdxlConfig, weights: dict, batch: int, laten
     for level in range(levels):
         prefix = f"down_blocks.{level}"
         for i in range(cfg.layers_per_block):
-            skips.append(unit(model, W, cfg, skips[-1], silu_temb, context, prefix, i, level))
+            skips.append(unit(model, W, cfg, skips[-1], silu_temb, context, prefix, i, level, kv_all))
         if level != levels - 1:
             skips.append(Layers.Conv2d(model, skips[-1], W(f"{prefix}.downsamplers.0.conv.weight"),
                                        W(f"{prefix}.downsamplers.0.conv.bias", "norm"), stride=2, padding=1))
 
     x = resnet_block(model, W, cfg, skips[-1], silu_temb, "mid_block.resnets.0")
-    x = transformer2d(model, W, cfg, x, context, "mid_block.attentions.0", cfg.heads[-1], cfg.transformer_layers[-1])
+    x = transformer2d(model, W, cfg, x, context, "mid_block.attentions.0", cfg.heads[-1], cfg.transformer_layers[-1],
+                      kv_all)
     x = resnet_block(model, W, cfg, x, silu_temb, "mid_block.resnets.1")
 
     for i in range(levels):
@@ -319,7 +349,7 @@ def build_unet(device: Device, cfg: SdxlConfig, weights: dict, batch: int, laten
         prefix = f"up_blocks.{i}"
         for j in range(cfg.layers_per_block + 1):
             x = Ops.Join([x, skips.pop()], 1)
-            x = unit(model, W, cfg, x, silu_temb, context, prefix, j, level)
+            x = unit(model, W, cfg, x, silu_temb, context, prefix, j, level, kv_all)
         if i != levels - 1:
             nxt = skips[-1].Shape
             x = Layers.Conv2d(model, Layers.CropTo(Layers.UpsampleNearest(x), nxt[2], nxt[3]),
