@@ -108,7 +108,7 @@ __device__ __forceinline__ float4 load4_vec(const void* p, int dt, int64_t off) 
   return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
 }
 
-__device__ __forceinline__ bool aligned16(const void* p, int64_t elems_a, int64_t elems_b, int es) {
+__host__ __device__ __forceinline__ bool aligned16(const void* p, int64_t elems_a, int64_t elems_b, int es) {
   return (uintptr_t)p % 16 == 0 && (elems_a * es) % 16 == 0 && (elems_b * es) % 16 == 0;
 }
 
@@ -212,9 +212,22 @@ struct EpiLane {
   bool fast, out_vec, gate_rows;
 };
 
+// Orders a wave's LDS writes before its later LDS reads (and those reads
+// before its next writes) without meeting the other waves: a wave's LDS
+// instructions execute in issue order, so only the compiler must be kept
+// from moving them across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // One 32-row slice (accumulator row block i of the wave) through LDS, so
 // the epilogue walks rows of four consecutive outputs and every global
-// store is a vector. On the fast path (a linear epilogue, every column of
+// store is a vector. The stage is the wave's own (the caller's workgroup
+// barrier after the K loop freed the tiles it overlaps), so the slices sync
+// per wave and the waves' epilogues run apart: one wave's residual loads
+// overlap another's stores. On the fast path (a linear epilogue, every column of
 // the wave in range, aligned rows) the loop is unrolled so that the slice's
 // residual and row-bias loads all go out before its first store, and their
 // latency is paid once per slice rather than once per row. Anything else
@@ -246,7 +259,7 @@ __device__ __forceinline__ void epilogue_slice(const GemmArgs& a, int64_t bidx, 
   for (int j = 0; j < TN; j++)
 #pragma unroll
     for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[j][r];
-  __syncthreads();
+  wave_lds_sync();
   if (L.fast) {
 #pragma unroll
     for (int t = 0; t < IT; t++) {
@@ -264,7 +277,7 @@ __device__ __forceinline__ void epilogue_slice(const GemmArgs& a, int64_t bidx, 
                    L.out_vec, L.gate_rows);
     }
   }
-  __syncthreads();
+  wave_lds_sync();
 }
 
 // Slices I .. TM - 1, expanded at compile time so every accumulator index
@@ -446,6 +459,203 @@ __device__ __forceinline__ void staged_epilogue(const GemmArgs& a, int64_t bidx,
   epilogue_slices<0, TM, TN, WN>(a, bidx, L, acc, stage, row0);
 }
 
+// ---- The fast epilogue ------------------------------------------------------
+//
+// The same staging as staged_epilogue, for launches whose every wave column
+// is in range, whose output (and residual, of the output's type) rows are
+// 16-byte aligned, whose gate is one row and whose epilogue is linear (bias,
+// row bias, residual, gated residual) or an activation (epi_fast_ok). The
+// output type and the mode are decided once per wave, so each slice is one
+// straight run of code: an epilogue with a type or mode test per row left
+// taken branches all through it, and refetching that code cost 16-18 us per
+// 256 x 256 tile (2 us straight).
+
+// Four consecutive values at byte offset off of a bounds-checked buffer,
+// widened to fp32 (zeros past its end).
+template <typename OT>
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(OT) == 4) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  } else {
+    const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    const OT* h = (const OT*)&u;
+    return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+  }
+}
+// Stores four consecutive outputs at byte offset off (dropped past the
+// buffer's end).
+template <typename OT>
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[4]) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  if constexpr (sizeof(OT) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, make_float4(v[0], v[1], v[2], v[3])), r, off, 0, 0);
+  } else {
+    OT h[4] = {(OT)v[0], (OT)v[1], (OT)v[2], (OT)v[3]};
+    __builtin_amdgcn_raw_buffer_store_b64(*(const u32x2*)h, r, off, 0, 0);
+  }
+}
+
+enum FastMode { FM_PLAIN, FM_RESID, FM_ACT };
+
+// The row bias of rows row0 + t * step (zeros without one; rows past M
+// read row M - 1, whose outputs are dropped).
+template <int IT>
+__device__ __forceinline__ void load_row_bias(const GemmArgs& a, int row0, int step, float (&rb)[IT]) {
+  const int dt = a.row_bias_dtype;
+  if (!a.row_bias) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) rb[t] = 0.f;
+  } else if (dt == NDX_F32) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) rb[t] = ((const float*)a.row_bias)[min(row0 + t * step, a.M - 1)];
+  } else if (dt == NDX_F16) {
+#pragma unroll
+    for (int t = 0; t < IT; t++) rb[t] = (float)((const _Float16*)a.row_bias)[min(row0 + t * step, a.M - 1)];
+  } else {
+#pragma unroll
+    for (int t = 0; t < IT; t++) rb[t] = (float)((const __bf16*)a.row_bias)[min(row0 + t * step, a.M - 1)];
+  }
+}
+
+// One 32-row slice of the fast epilogue. T is the product's type (the
+// residual adds the product rounded to it), OT the output's. The output
+// and the residual are buffers ending at row M: a row past M stores
+// nothing and reads zeros with no branch, so the stores of a slice go out
+// back to back (a per-row branch made the compiler wait for each store
+// before the next).
+template <int TN, int WN, typename T, typename OT, int MODE>
+__device__ __forceinline__ void fast_slice(const GemmArgs& a, int64_t bidx, const EpiLane& L, f32x16 (&acc)[TN],
+                                           float* stage, int row0) {
+  constexpr int CS = WN + 4, C4 = WN / 4, RSTEP = 64 / C4, IT = 32 / RSTEP;
+  constexpr int ES = (int)sizeof(OT);
+  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc((const OT*)a.c + bidx * a.batch_c, (uint32_t)(int64_t(a.M) * a.ldc * ES));
+  float4 res[MODE == FM_RESID ? IT : 1];
+  float rb[IT];
+  if constexpr (MODE == FM_RESID) {
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc((const OT*)a.resid + bidx * a.batch_r, (uint32_t)(int64_t(a.M) * a.ldr * ES));
+#pragma unroll
+    for (int t = 0; t < IT; t++) {
+      const int row = row0 + L.rl0 + t * RSTEP;
+      res[t] = buf_load4<OT>(rr, uint32_t((row * a.ldr + L.col) * ES));
+    }
+  }
+  load_row_bias(a, row0 + L.rl0, RSTEP, rb);
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[j][r];
+  wave_lds_sync();
+  if constexpr (MODE == FM_ACT) {
+    // Rolled loops, one per activation (their code is long).
+    const int ep = a.epilogue;
+    auto act_rows = [&](auto f) __attribute__((always_inline)) {
+#pragma unroll 1
+      for (int t = 0; t < IT; t++) {
+        const int rl = L.rl0 + t * RSTEP, row = row0 + rl;
+        const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
+        float b = 0.f;
+#pragma unroll
+        for (int u = 0; u < IT; u++) b = u == t ? rb[u] : b;
+        float x[4] = {f(v.x + L.bias.x + b), f(v.y + L.bias.y + b), f(v.z + L.bias.z + b), f(v.w + L.bias.w + b)};
+        buf_store4<OT>(rc, uint32_t((row * a.ldc + L.col) * ES), x);
+      }
+    };
+    if (ep == EPI_GELU_TANH) act_rows([](float x) { return gelu_tanh_f(x); });
+    else if (ep == EPI_GELU) act_rows([](float x) { return gelu_f(x); });
+    else act_rows([](float x) { return silu_f(x); });
+  } else {
+#pragma unroll
+    for (int t = 0; t < IT; t++) {
+      const int rl = L.rl0 + t * RSTEP, row = row0 + rl;
+      const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
+      float x[4] = {v.x + L.bias.x + rb[t], v.y + L.bias.y + rb[t], v.z + L.bias.z + rb[t], v.w + L.bias.w + rb[t]};
+      if constexpr (MODE == FM_RESID) {
+        const float4 g = row >= a.gate_split ? L.gate2 : L.gate;
+        x[0] = res[t].x + g.x * (float)(T)x[0];
+        x[1] = res[t].y + g.y * (float)(T)x[1];
+        x[2] = res[t].z + g.z * (float)(T)x[2];
+        x[3] = res[t].w + g.w * (float)(T)x[3];
+      }
+      buf_store4<OT>(rc, uint32_t((row * a.ldc + L.col) * ES), x);
+    }
+  }
+  wave_lds_sync();
+}
+
+template <int I, int TM, int TN, int WN, typename T, typename OT, int MODE>
+__device__ __forceinline__ void fast_slices(const GemmArgs& a, int64_t bidx, const EpiLane& L, f32x16 (&acc)[TM][TN],
+                                            float* stage, int row0) {
+  if constexpr (I < TM) {
+    fast_slice<TN, WN, T, OT, MODE>(a, bidx, L, acc[I], stage, row0 + I * 32);
+    fast_slices<I + 1, TM, TN, WN, T, OT, MODE>(a, bidx, L, acc, stage, row0);
+  }
+}
+
+template <int TM, int TN, int WN, typename T, typename OT>
+__device__ __forceinline__ void fast_epilogue_typed(const GemmArgs& a, int64_t bidx, const EpiLane& L,
+                                                    f32x16 (&acc)[TM][TN], float* stage, int row0) {
+  const int ep = a.epilogue;
+  if (ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL)
+    fast_slices<0, TM, TN, WN, T, OT, FM_RESID>(a, bidx, L, acc, stage, row0);
+  else if (ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU)
+    fast_slices<0, TM, TN, WN, T, OT, FM_ACT>(a, bidx, L, acc, stage, row0);
+  else
+    fast_slices<0, TM, TN, WN, T, OT, FM_PLAIN>(a, bidx, L, acc, stage, row0);
+}
+
+template <int TM, int TN, int WN, typename T>
+__device__ __forceinline__ void fast_epilogue(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][TN], float* stage,
+                                              int row0, int col0) {
+  constexpr int C4 = WN / 4;
+  const int lane = threadIdx.x & 63;
+  EpiLane L;
+  L.c4 = lane % C4;
+  L.rl0 = lane / C4;
+  L.col = col0 + L.c4 * 4;
+  L.n = 4;
+  L.fast = true;
+  L.out_vec = true;
+  L.gate_rows = false;
+  L.bias = a.bias ? load_cols(a.bias, a.bias_dtype, L.col, 4, (uintptr_t)a.bias % 16 == 0) : make_float4(0.f, 0.f, 0.f, 0.f);
+  L.gate = make_float4(1.f, 1.f, 1.f, 1.f);
+  L.gate2 = L.gate;
+  if (a.epilogue == EPI_GATED_RESIDUAL) {
+    const int gs = dtype_size(a.gate_dtype);
+    L.gate = load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + L.col, 4, aligned16(a.gate, a.batch_gate, 0, gs));
+    L.gate2 = a.gate_split_off == 0
+                  ? L.gate
+                  : load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + a.gate_split_off + L.col, 4,
+                              aligned16(a.gate, a.batch_gate, a.gate_split_off, gs));
+  }
+  if (a.c_dtype == NDX_F32) fast_epilogue_typed<TM, TN, WN, T, float>(a, bidx, L, acc, stage, row0);
+  else if (a.c_dtype == NDX_BF16) fast_epilogue_typed<TM, TN, WN, T, __bf16>(a, bidx, L, acc, stage, row0);
+  else fast_epilogue_typed<TM, TN, WN, T, _Float16>(a, bidx, L, acc, stage, row0);
+}
+
+// Whether a launch may take fast_epilogue with tiles BN wide.
+static bool epi_fast_ok(const GemmArgs& a, int bn) {
+  if (a.M == 0) return true;  // the absent second product of a launch
+  const int ep = a.epilogue;
+  const bool residual = ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL;
+  if (!(ep == EPI_NONE || ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU || residual)) return false;
+  if (a.c_dtype != NDX_F32 && a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16) return false;
+  if (a.N % bn) return false;
+  if (!aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype))) return false;
+  if (residual && (a.r_dtype != a.c_dtype || !aligned16(a.resid, a.ldr, a.batch_r, dtype_size(a.r_dtype)))) return false;
+  if (ep == EPI_GATED_RESIDUAL && a.ldg != 0) return false;
+  // Output and residual rows are addressed by 32-bit byte offsets from the
+  // batch's first row; a row at or past M must lie past the buffer's end.
+  const int64_t lim = int64_t(1) << 31, es = dtype_size(a.c_dtype);
+  if (int64_t(a.M) * a.ldc * es >= lim || (residual && int64_t(a.M) * a.ldr * es >= lim)) return false;
+  if (a.ldc < a.N || (residual && a.ldr < a.N)) return false;
+  // Rows up to a tile past M stay below 2^32 bytes (no wrap into range).
+  if (a.ldc * es >= (int64_t(1) << 22) || (residual && a.ldr * es >= (int64_t(1) << 22))) return false;
+  return true;
+}
+
 // Element offset of 16-byte chunk c of row r in a swizzled [rows][64] tile
 // (128-byte rows). gfx950's LDS serves a ds_read_b128 sixteen lanes at a
 // time across 64 four-byte banks (256 bytes); the fragment reads have those
@@ -612,7 +822,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
 // a0 and a1 are two products with the same N, K and batch run as one grid
 // (a0's row tiles first, then a1's); a1.M = 0 for a single product.
-template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN = false>
+template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN = false, bool FAST = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
                                                                                     int grid) {
   typedef typename MfmaOp<T>::V V;
@@ -841,9 +1051,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = MfmaOp<T>::mma(af[p][i], bf[p][j], acc[i][j]);
       // Schedule: the tile DMA first, then each step's MFMAs with the next
-      // fragments' LDS reads threaded between them.
+      // fragments' LDS reads threaded between them. With eight or more
+      // MFMAs a step, the reads go out in two early groups (after the
+      // second and the sixth MFMA), so each has most of the step to land
+      // before the next step's first MFMAs need it (qkv 1118 -> 1335
+      // TFLOP/s at 5376 x 9216 x 3072).
       if (s == 0) __builtin_amdgcn_sched_group_barrier(0x0010, A_LOADS + B_LOADS, 0);
-      if (NM >= NF) {
+      if constexpr (NM >= 8) {
+        __builtin_amdgcn_sched_group_barrier(0x0008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0100, NF / 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0100, NF - NF / 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0008, NM - 6, 0);
+      } else if (NM >= NF) {
 #pragma unroll
         for (int f = 0; f < NF; f++) {
           __builtin_amdgcn_sched_group_barrier(0x0008, NM / NF, 0);
@@ -860,7 +1080,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   __syncthreads();
 
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
-  staged_epilogue<TM, TN, WN, QKN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  if constexpr (FAST) fast_epilogue<TM, TN, WN, T>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  else staged_epilogue<TM, TN, WN, QKN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ---- int8 weights, direct to LDS ----------------------------------------------
@@ -1609,12 +1830,16 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
   int tiles = ((a.M + BM - 1) / BM + (a1.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   int grid = (tiles + 7) / 8 * 8;
   dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
+  const bool fast = epi_fast_ok(a, BN) && epi_fast_ok(a1, BN);
   // A convolution's K (taps x Cin, Cin a multiple of BK) is always whole.
   if constexpr (CONV) {
-    if (a.a_dtype == NDX_BF16)
-      hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, true, true>), g, b, 0, s, a, a1, grid);
-    else
-      hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, true, true>), g, b, 0, s, a, a1, grid);
+    if (a.a_dtype == NDX_BF16) {
+      if (fast) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, true, true, false, true>), g, b, 0, s, a, a1, grid);
+      else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, true, true>), g, b, 0, s, a, a1, grid);
+    } else {
+      if (fast) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, true, true, false, true>), g, b, 0, s, a, a1, grid);
+      else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, true, true>), g, b, 0, s, a, a1, grid);
+    }
   } else {
     const bool kfull = a.K % BK == 0;
     if constexpr (WN == 64) {
@@ -1629,10 +1854,12 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
       }
     }
     if (a.a_dtype == NDX_BF16) {
-      if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true>), g, b, 0, s, a, a1, grid);
+      if (kfull && fast) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true, false, true>), g, b, 0, s, a, a1, grid);
+      else if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true>), g, b, 0, s, a, a1, grid);
       else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, false>), g, b, 0, s, a, a1, grid);
     } else {
-      if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true>), g, b, 0, s, a, a1, grid);
+      if (kfull && fast) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true, false, true>), g, b, 0, s, a, a1, grid);
+      else if (kfull) hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true>), g, b, 0, s, a, a1, grid);
       else hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, false>), g, b, 0, s, a, a1, grid);
     }
   }
