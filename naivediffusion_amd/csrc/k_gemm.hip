@@ -1102,7 +1102,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
 // ends. The six tiles (A, int8 and bf16, two of each) are distinct restrict
 // pointers and the loop is unrolled by two, so no LDS read waits for a DMA
 // into another tile; at 256 x 256 they fill the 160 KB of LDS.
-template <int BM, int BN, int WM, int WN, typename T, bool SF16>
+template <int BM, int BN, int WM, int WN, typename T, bool SF16, bool FAST>
 __device__ __forceinline__ void gemm_w8_body(const GemmArgs& a, int grid, T* __restrict__ A0, T* __restrict__ A1,
                                              int8_t* __restrict__ Q0, int8_t* __restrict__ Q1,
                                              T* __restrict__ B0, T* __restrict__ B1, float* stage_all) {
@@ -1309,7 +1309,8 @@ __device__ __forceinline__ void gemm_w8_body(const GemmArgs& a, int grid, T* __r
       w -= caps[t];
     }
   }
-  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  if constexpr (FAST) fast_epilogue<TM, TN, WN, T>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  else staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // Every tile is an LDS array of its own: the compiler orders an LDS access
@@ -1318,7 +1319,7 @@ __device__ __forceinline__ void gemm_w8_body(const GemmArgs& a, int grid, T* __r
 // tile waits for the DMA into another. At 256 x 256 the six tiles fill the
 // 160 KB of LDS; the epilogue stages in the tiles wherever they can hold
 // every wave's stage.
-template <int BM, int BN, int WM, int WN, typename T, bool SF16>
+template <int BM, int BN, int WM, int WN, typename T, bool SF16, bool FAST>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel(GemmArgs a, int grid) {
   constexpr int NW = (BM / WM) * (BN / WN);
   constexpr int TILES = 2 * (BM * BK * (int)sizeof(T) + BN * BK + BN * BK * (int)sizeof(T));
@@ -1332,10 +1333,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_w8_lds_kernel
   __shared__ __attribute__((aligned(1024))) T b0[BN * BK];
   __shared__ __attribute__((aligned(1024))) T b1[BN * BK];
   if constexpr (CAP >= NW) {
-    gemm_w8_body<BM, BN, WM, WN, T, SF16>(a, grid, a0, a1, q0, q1, b0, b1, nullptr);
+    gemm_w8_body<BM, BN, WM, WN, T, SF16, FAST>(a, grid, a0, a1, q0, q1, b0, b1, nullptr);
   } else {
     __shared__ __attribute__((aligned(1024))) float st[NW * SWB / 4];
-    gemm_w8_body<BM, BN, WM, WN, T, SF16>(a, grid, a0, a1, q0, q1, b0, b1, st);
+    gemm_w8_body<BM, BN, WM, WN, T, SF16, FAST>(a, grid, a0, a1, q0, q1, b0, b1, st);
   }
 }
 
@@ -1941,14 +1942,20 @@ static void launch_w8_lds(const GemmArgs& a, hipStream_t s) {
   int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   int grid = (tiles + 7) / 8 * 8;
   dim3 g(grid, a.batch), b((BM / WM) * (BN / WN) * 64);
-  const bool f16s = a.s_dtype == NDX_F16;
+  const bool f16s = a.s_dtype == NDX_F16, fast = epi_fast_ok(a, BN);
+#define NDX_W8(TT, SF)                                                                                        \
+  do {                                                                                                        \
+    if (fast) hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, TT, SF, true>), g, b, 0, s, a, grid);  \
+    else hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, TT, SF, false>), g, b, 0, s, a, grid);      \
+  } while (0)
   if (a.a_dtype == NDX_BF16) {
-    if (f16s) hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, __bf16, true>), g, b, 0, s, a, grid);
-    else hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, __bf16, false>), g, b, 0, s, a, grid);
+    if (f16s) NDX_W8(__bf16, true);
+    else NDX_W8(__bf16, false);
   } else {
-    if (f16s) hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, _Float16, true>), g, b, 0, s, a, grid);
-    else hipLaunchKernelGGL((gemm_w8_lds_kernel<BM, BN, WM, WN, _Float16, false>), g, b, 0, s, a, grid);
+    if (f16s) NDX_W8(_Float16, true);
+    else NDX_W8(_Float16, false);
   }
+#undef NDX_W8
 }
 
 static bool is_lds_kind(GemmKind k) {
