@@ -1511,11 +1511,15 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     n = fused;
   }
 
-  // Off unless NDX_FUSE_QK_NORM=1 (read at compile time): on the MMDiT
-  // step the fused epilogue costs the 256x256 QKV product more (383 against
-  // 310 us a launch) than the two head-norm passes it removes (27 us).
+  // By default only where the product runs on the 256x256 tile with one head
+  // per wave (gemm_qk_norm_fast): there the fused epilogue is a straight run
+  // of shuffles and the two head-norm passes go away. On the narrower tiles
+  // each head spans two waves that meet in LDS four times a slice, which
+  // costs the product more than the passes it removes; NDX_FUSE_QK_NORM=1
+  // (read at compile time) fuses there too, NDX_FUSE_QK_NORM=0 nowhere.
   const char* fuse_qk_env = getenv("NDX_FUSE_QK_NORM");
-  const bool fuse_qk = fuse_qk_env && fuse_qk_env[0] == '1';
+  const bool fuse_any = fuse_qk_env && fuse_qk_env[0] == '1';
+  const bool fuse_qk = !(fuse_qk_env && fuse_qk_env[0] == '0');
   // Rewrite: the head norm + rotation of the q and k thirds of a QKV
   // projection (Rotate(HeadNorm(Linear(x))), QwenImageDit.cs:342-347;
   // Transformer.cs:37-64) runs in the projection's epilogue
@@ -1593,6 +1597,7 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
     p.K = (int)xv.v.size[3];
     p.batch = (int)(xv.v.size[0] * xv.v.size[1]);
     p.tile_hint = second_stream_tile(L, p.M);
+    if (!fuse_any && !gemm_qk_norm_fast(p, (int)(2 * D))) continue;
     if (!gemm_qk_norm_ok(p, (int)(2 * D))) {
       // Where the chosen tile's waves do not hold half a head, the 64x128
       // or the 128x128 tile: the fusion then does not depend on which

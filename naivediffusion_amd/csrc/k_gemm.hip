@@ -606,6 +606,97 @@ __device__ __forceinline__ void fast_epilogue_typed(const GemmArgs& a, int64_t b
     fast_slices<0, TM, TN, WN, T, OT, FM_PLAIN>(a, bidx, L, acc, stage, row0);
 }
 
+// EPI_QK_NORM_ROPE on waves 128 columns wide: each wave's columns are one
+// whole head of q or k (or v columns, which take the plain path). Per row:
+// the product plus bias rounded to the output type, its sum of squares over
+// the head (the lane's four, then lanes ^1, ^2, ^4, ^8: 64 columns, then
+// ^16: the other 64, the summation order of two 64-column halves), the
+// RMS-normalised values times the weight rounded again (the head norm's
+// output), then the rotate-half rotation in fp32 with the partner value
+// (dim +- 64) from lane ^ 16 and the row's rotary table entry
+// (Transformer.cs:37-64). No LDS beyond the wave's own stage and no
+// barrier: the wave runs its epilogue alone, as fast_slice does.
+template <int TN, typename OT, bool ROT>
+__device__ __forceinline__ void fast_qkn_slice(const GemmArgs& a, int64_t bidx, const EpiLane& L, f32x16 (&acc)[TN],
+                                               float* stage, int row0, const float (&w)[4]) {
+  constexpr int WN = 128, CS = WN + 4, C4 = WN / 4, RSTEP = 64 / C4, IT = 32 / RSTEP, HALF = 8;
+  constexpr int ES = (int)sizeof(OT);
+  const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc((const OT*)a.c + bidx * a.batch_c, (uint32_t)(int64_t(a.M) * a.ldc * ES));
+  const int dim = L.col & 127;
+  const bool high = dim >= 64;
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lhalf + (r & 3)) * CS + j * 32 + lrow] = acc[j][r];
+  wave_lds_sync();
+#pragma unroll
+  for (int h = 0; h < IT; h += HALF) {
+    // The rotary rows of these rows (rows past M read row M - 1).
+    float4 cs[HALF], sn[HALF];
+    if constexpr (ROT) {
+#pragma unroll
+      for (int t = 0; t < HALF; t++) {
+        const int64_t row = min(row0 + L.rl0 + (h + t) * RSTEP, a.M - 1);
+        cs[t] = *(const float4*)(a.rope_cos + row * 64 + (dim & 63));
+        sn[t] = *(const float4*)(a.rope_sin + row * 64 + (dim & 63));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < HALF; t++) {
+      const int rl = L.rl0 + (h + t) * RSTEP, row = row0 + rl;
+      const float4 sv = *(const float4*)&stage[rl * CS + L.c4 * 4];
+      const float v[4] = {(float)(OT)(sv.x + L.bias.x), (float)(OT)(sv.y + L.bias.y), (float)(OT)(sv.z + L.bias.z),
+                          (float)(OT)(sv.w + L.bias.w)};
+      float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      ss += __shfl_xor(ss, 16, 64);
+      const float r = 1.0f / sqrtf(ss * (1.0f / 128) + a.norm_eps);
+      float n[4], y[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) n[e] = (float)(OT)(v[e] * r * w[e]);
+      if constexpr (ROT) {
+        const float cc[4] = {cs[t].x, cs[t].y, cs[t].z, cs[t].w}, sx[4] = {sn[t].x, sn[t].y, sn[t].z, sn[t].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float pv = __shfl_xor(n[e], 16, 64);
+          y[e] = high ? n[e] * cc[e] + pv * sx[e] : n[e] * cc[e] - pv * sx[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = n[e];
+      }
+      buf_store4<OT>(rc, uint32_t((row * a.ldc + L.col) * ES), y);
+    }
+  }
+  wave_lds_sync();
+}
+
+template <int I, int TM, int TN, typename OT, bool ROT>
+__device__ __forceinline__ void fast_qkn_slices(const GemmArgs& a, int64_t bidx, const EpiLane& L,
+                                                f32x16 (&acc)[TM][TN], float* stage, int row0, const float (&w)[4]) {
+  if constexpr (I < TM) {
+    fast_qkn_slice<TN, OT, ROT>(a, bidx, L, acc[I], stage, row0 + I * 32, w);
+    fast_qkn_slices<I + 1, TM, TN, OT, ROT>(a, bidx, L, acc, stage, row0, w);
+  }
+}
+
+template <int TM, int TN, typename OT>
+__device__ __forceinline__ void fast_qkn(const GemmArgs& a, int64_t bidx, const EpiLane& L, f32x16 (&acc)[TM][TN],
+                                         float* stage, int row0, int col0) {
+  // The weight of the wave's head (q or k), picked by arithmetic (a select
+  // between two argument fields would copy the block to scratch).
+  const uintptr_t wq = (uintptr_t)a.norm_q, wk = (uintptr_t)a.norm_k;
+  const void* nw = (const void*)(wq + uintptr_t(col0 >= a.qk_cols / 2) * (wk - wq));
+  float w[4];
+  const int dim = L.col & 127;
+#pragma unroll
+  for (int e = 0; e < 4; e++) w[e] = nw ? load_f(nw, a.norm_dtype, dim + e) : 1.f;
+  if (a.rope_cos) fast_qkn_slices<0, TM, TN, OT, true>(a, bidx, L, acc, stage, row0, w);
+  else fast_qkn_slices<0, TM, TN, OT, false>(a, bidx, L, acc, stage, row0, w);
+}
+
 template <int TM, int TN, int WN, typename T>
 __device__ __forceinline__ void fast_epilogue(const GemmArgs& a, int64_t bidx, f32x16 (&acc)[TM][TN], float* stage,
                                               int row0, int col0) {
@@ -630,17 +721,29 @@ __device__ __forceinline__ void fast_epilogue(const GemmArgs& a, int64_t bidx, f
                   : load_cols(a.gate, a.gate_dtype, bidx * a.batch_gate + a.gate_split_off + L.col, 4,
                               aligned16(a.gate, a.batch_gate, a.gate_split_off, gs));
   }
+  if constexpr (WN == 128) {
+    // Uniform over the workgroup: qk_cols is a multiple of the tile width.
+    if (a.epilogue == EPI_QK_NORM_ROPE && col0 < a.qk_cols) {
+      if (a.c_dtype == NDX_F32) fast_qkn<TM, TN, float>(a, bidx, L, acc, stage, row0, col0);
+      else if (a.c_dtype == NDX_BF16) fast_qkn<TM, TN, __bf16>(a, bidx, L, acc, stage, row0, col0);
+      else fast_qkn<TM, TN, _Float16>(a, bidx, L, acc, stage, row0, col0);
+      return;
+    }
+  }
   if (a.c_dtype == NDX_F32) fast_epilogue_typed<TM, TN, WN, T, float>(a, bidx, L, acc, stage, row0);
   else if (a.c_dtype == NDX_BF16) fast_epilogue_typed<TM, TN, WN, T, __bf16>(a, bidx, L, acc, stage, row0);
   else fast_epilogue_typed<TM, TN, WN, T, _Float16>(a, bidx, L, acc, stage, row0);
 }
 
-// Whether a launch may take fast_epilogue with tiles BN wide.
-static bool epi_fast_ok(const GemmArgs& a, int bn) {
+// Whether a launch may take fast_epilogue with tiles BN wide (QKN: the
+// fused head norm on 128-column waves).
+static bool epi_fast_ok(const GemmArgs& a, int bn, bool qkn = false) {
   if (a.M == 0) return true;  // the absent second product of a launch
   const int ep = a.epilogue;
   const bool residual = ep == EPI_GATED_RESIDUAL || ep == EPI_RESIDUAL;
-  if (!(ep == EPI_NONE || ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU || residual)) return false;
+  if (!(ep == EPI_NONE || ep == EPI_GELU_TANH || ep == EPI_GELU || ep == EPI_SILU || residual ||
+        (qkn && ep == EPI_QK_NORM_ROPE && a.qk_cols % 128 == 0)))
+    return false;
   if (a.c_dtype != NDX_F32 && a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16) return false;
   if (a.N % bn) return false;
   if (!aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype))) return false;
@@ -1843,6 +1946,18 @@ static void launch_mfma_lds(const GemmArgs& a, hipStream_t s, const GemmArgs* se
     }
   } else {
     const bool kfull = a.K % BK == 0;
+    if constexpr (WN == 128 && BM == 256) {
+      // The fused head norm on whole heads per wave (the fast epilogue).
+      if (a.epilogue == EPI_QK_NORM_ROPE) {
+        if (a.a_dtype == NDX_BF16)
+          hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, __bf16, false, true, true, true>), g, b, 0, s, a, a1,
+                             grid);
+        else
+          hipLaunchKernelGGL((gemm_mfma_lds_kernel<BM, BN, WM, WN, _Float16, false, true, true, true>), g, b, 0, s, a,
+                             a1, grid);
+        return;
+      }
+    }
     if constexpr (WN == 64) {
       // The fused head norm (whole K tiles only, one problem per launch).
       if (a.epilogue == EPI_QK_NORM_ROPE) {
@@ -1998,12 +2113,28 @@ const char* gemm_pair_family(const GemmArgs& a, const GemmArgs& b) {
   return gemm_family(both);
 }
 
+// The 256 x 256 tile runs the fused head norm on 8 waves of 64 x 128 (one
+// head per wave, fast_qkn) where the fast epilogue's conditions hold.
+static bool qkn_wide_ok(const GemmArgs& a, int qk_cols) {
+  GemmArgs q = a;
+  q.epilogue = EPI_QK_NORM_ROPE;
+  q.qk_cols = qk_cols;
+  return q.N % 256 == 0 && qk_cols % 128 == 0 && (!a.c || epi_fast_ok(q, 256, true));
+}
+
+bool gemm_qk_norm_fast(const GemmArgs& a, int qk_cols) {
+  if (qk_cols <= 0 || qk_cols % 128 || a.K % BK ||
+      (a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16 && a.c_dtype != NDX_F32))
+    return false;
+  return choose(a) == K_LDS_256W8 && qkn_wide_ok(a, qk_cols);
+}
+
 bool gemm_qk_norm_ok(const GemmArgs& a, int qk_cols) {
   if (qk_cols <= 0 || qk_cols % 128 || a.K % BK ||
       (a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16 && a.c_dtype != NDX_F32))
     return false;
   switch (choose(a)) {
-    case K_LDS_256W8: return qk_cols % 256 == 0;
+    case K_LDS_256W8: return qk_cols % 256 == 0 || qkn_wide_ok(a, qk_cols);
     case K_LDS_128:
     case K_LDS_64x128: return true;
     default: return false;
@@ -2040,7 +2171,10 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
-    case K_LDS_256W8: launch_mfma_lds<256, 256, 128, 64>(a, s); break;
+    case K_LDS_256W8:
+      if (a.epilogue == EPI_QK_NORM_ROPE && qkn_wide_ok(a, a.qk_cols)) launch_mfma_lds<256, 256, 64, 128>(a, s);
+      else launch_mfma_lds<256, 256, 128, 64>(a, s);
+      break;
     case K_LDS_128W8: launch_mfma_lds<128, 128, 64, 32>(a, s); break;
     case K_W8_256W8: launch_w8_lds<256, 256, 128, 64>(a, s); break;
     case K_W8_128: launch_w8_lds<128, 128, 64, 64>(a, s); break;

@@ -296,6 +296,9 @@ const char* conv_family(const ConvArgs& a);
 // EPI_QK_NORM_ROPE with qk_cols: a 16-bit direct-to-LDS tile of 64-column
 // waves whose width divides qk_cols.
 bool gemm_qk_norm_ok(const GemmArgs& a, int qk_cols);
+// Whether the fused head norm runs on the product's own (256 x 256) tile
+// with one head per wave: the form that costs the product nothing extra.
+bool gemm_qk_norm_fast(const GemmArgs& a, int qk_cols);
 void launch_elementwise(const ElemArgs& a, hipStream_t s);
 void launch_upsample(const UpsampleArgs& a, hipStream_t s);
 void launch_patch(const PatchArgs& a, hipStream_t s);
