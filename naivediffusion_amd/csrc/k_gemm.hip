@@ -1485,6 +1485,7 @@ __device__ __forceinline__ void load_w8(const GemmArgs& a, const char* W, int n,
 // Within a 16-wide K step, lane half h feeds k = h*8 + t to MFMA number t,
 // the same permutation for both operands, so eight MFMAs cover the step
 // from one 16-byte-pair LDS read per operand.
+template <bool FAST>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
   constexpr int BM = 128, BN = 128, WM = 64, WN = 64, TM = 2, TN = 2;
   constexpr int TILE_BYTES = 2 * (BM + BN) * BK32 * 4;
@@ -1590,7 +1591,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a, int grid) {
     __syncthreads();
   }
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
-  staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  if constexpr (FAST) fast_epilogue<TM, TN, WN, float>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+  else staged_epilogue<TM, TN, WN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
 }
 
 // ---- GEMV ---------------------------------------------------------------------
@@ -2183,7 +2185,8 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_F32: {
       int tiles = ((a.M + 127) / 128) * ((a.N + 127) / 128);
       int grid = (tiles + 7) / 8 * 8;
-      hipLaunchKernelGGL(gemm_f32_kernel, dim3(grid, a.batch), dim3(256), 0, s, a, grid);
+      if (epi_fast_ok(a, 128)) hipLaunchKernelGGL(gemm_f32_kernel<true>, dim3(grid, a.batch), dim3(256), 0, s, a, grid);
+      else hipLaunchKernelGGL(gemm_f32_kernel<false>, dim3(grid, a.batch), dim3(256), 0, s, a, grid);
       break;
     }
     default: {
