@@ -10,7 +10,7 @@ restatement of the reference's C# CPU layer path, timed on this host over one
 block of the same step and scaled to 60 blocks). The per-family breakdown
 comes from one untimed step with every kernel bracketed.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--compute bf16|f32|f16] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--int8] [--compute bf16|f32|f16] [--no-cpu-baseline] [--no-replay]
     python bench.py --workload anima|sdxl|qwen   # the Anima DiT / SDXL UNet / Qwen-Image 2.1 steps
     python bench.py --calibrate-copy    # a plain 1 GiB device copy, for scaling HBM counters
 
@@ -456,6 +456,9 @@ def main():
     ap.add_argument("--one-stream", action="store_true", help="mmdit: the text stream on the image stream's "
                     "stream (default: its own, beside the image stream)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-replay", action="store_true",
+                    help="skip the steps replayed from one captured HIP graph (for profiler runs: rocprofv3's "
+                         "kernel trace of the SDXL step's capture ended the process on the host)")
     ap.add_argument("--calibrate-copy", action="store_true", help="run only the 1 GiB copy used to scale counters")
     args = ap.parse_args()
 
@@ -488,7 +491,7 @@ def main():
         f"{compiled.PersistentSize / 1e9:.1f} GB weights, {compiled.TemporarySize / 1e9:.2f} GB scratch")
 
     s_per_step, prof, dominant = measure(dev, compiled, setup["inputs"], setup["out"], args.steps, args.warmup)
-    replay_s = measure_replay(dev, compiled, setup["inputs"], setup["out"], args.steps)
+    replay_s = None if args.no_replay else measure_replay(dev, compiled, setup["inputs"], setup["out"], args.steps)
     peak = FP32_PEAK_TFLOPS if args.compute == "f32" else MFMA_BF16_PEAK_TFLOPS
     total_flops = sum(e["flops"] for e in prof.values())
     kernel_ms = sum(e["ms"] for e in prof.values())
@@ -508,7 +511,7 @@ def main():
         "step_frac_of_mfma_peak": total_flops / s_per_step / 1e12 / peak,
         "kernel_ms_per_step": kernel_ms,
         # the same steps replayed from one captured HIP graph, no events (value: the event-bracketed run above)
-        "graph_replay_ms_per_step": replay_s * 1e3,
+        "graph_replay_ms_per_step": None if replay_s is None else replay_s * 1e3,
     })
     result = {
         "metric": setup["metric"],
