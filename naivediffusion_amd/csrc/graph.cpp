@@ -97,11 +97,11 @@ int64_t numel4(const View4& v) { return v.size[0] * v.size[1] * v.size[2] * v.si
 // tiles do the same work in about two thirds of the CU time of 64x64 ones
 // (the MMDiT text stream: 2% less step time on MI355X; 256x256 tiles hold
 // CUs so long that the other stream's rounds stall).
-// NDX_SECOND_STREAM_TILE=1..4 (256x256, 128x128, 64x128, 64x64) pins it,
+// NDX_SECOND_STREAM_TILE=1..5 (256x256, 128x128, 64x128, 64x64, the register-capped 64x64) pins it,
 // read at compile time, for sweeps.
 int second_stream_tile(const GNode& n, int64_t rows) {
   if (n.lane != 1 || rows < 128) return 0;
-  if (const char* pin = getenv("NDX_SECOND_STREAM_TILE"); pin && pin[0] >= '1' && pin[0] <= '4' && !pin[1])
+  if (const char* pin = getenv("NDX_SECOND_STREAM_TILE"); pin && pin[0] >= '1' && pin[0] <= '5' && !pin[1])
     return pin[0] - '0';
   return 2;
 }
@@ -2531,6 +2531,8 @@ void compute_families(ndx_model* m) {
     p.batch = (int)(x.v.size[0] * x.v.size[1]);
     p.tile_hint = k.tile_hint ? k.tile_hint : second_stream_tile(k, p.M);
     p.c_dtype = m->values[k.out].dtype;
+    p.epilogue = k.i0;
+    if (k.in.size() > 4 && k.in[4] >= 0) p.r_dtype = m->values[k.in[4]].dtype;
     return p;
   };
   // NDX_PROFILE_LANES=1 names the second stream's kernels apart ("@lane1"),

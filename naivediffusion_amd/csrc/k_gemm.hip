@@ -746,6 +746,9 @@ static bool epi_fast_ok(const GemmArgs& a, int bn, bool qkn = false) {
     return false;
   if (a.c_dtype != NDX_F32 && a.c_dtype != NDX_BF16 && a.c_dtype != NDX_F16) return false;
   if (a.N % bn) return false;
+  if (residual && a.r_dtype != a.c_dtype) return false;
+  // Without pointers (a kernel family named before a run) the shape decides.
+  if (!a.c) return true;
   if (!aligned16(a.c, a.ldc, a.batch_c, dtype_size(a.c_dtype))) return false;
   if (residual && (a.r_dtype != a.c_dtype || !aligned16(a.resid, a.ldr, a.batch_r, dtype_size(a.r_dtype)))) return false;
   if (ep == EPI_GATED_RESIDUAL && a.ldg != 0) return false;
@@ -925,9 +928,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
 // a0 and a1 are two products with the same N, K and batch run as one grid
 // (a0's row tiles first, then a1's); a1.M = 0 for a single product.
-template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN = false, bool FAST = false>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
-                                                                                    int grid) {
+template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN, bool FAST>
+__device__ __forceinline__ void gemm_lds_body(const GemmArgs& a0, const GemmArgs& a1, int grid) {
   typedef typename MfmaOp<T>::V V;
   constexpr int WAVES_N = BN / WN;
   constexpr int NW = (BM / WM) * (BN / WN);
@@ -1185,6 +1187,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kern
   float* stage = reinterpret_cast<float*>(smem) + wave * 32 * (WN + 4);
   if constexpr (FAST) fast_epilogue<TM, TN, WN, T>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
   else staged_epilogue<TM, TN, WN, QKN>(a, bidx, acc, stage, m0 + wm * WM, n0 + wn * WN);
+}
+
+template <int BM, int BN, int WM, int WN, typename T, bool CONV, bool KFULL, bool QKN = false, bool FAST = false>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_lds_kernel(GemmArgs a0, GemmArgs a1,
+                                                                                    int grid) {
+  gemm_lds_body<BM, BN, WM, WN, T, CONV, KFULL, QKN, FAST>(a0, a1, grid);
+}
+
+// The 64 x 64 tile capped at 64 registers a lane (eight waves a SIMD), for a
+// product on the second stream: beside a 256 x 256 workgroup (two waves a
+// SIMD of about 220 registers, 128 KB of LDS) a CU has 64 registers a SIMD
+// lane and 32 KB of LDS left, so this tile runs next to it instead of
+// waiting for the CU. Whole K tiles and the fast epilogue only.
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(64))) void gemm_slim_kernel(GemmArgs a0, GemmArgs a1, int grid) {
+  gemm_lds_body<64, 64, 32, 32, T, false, true, false, true>(a0, a1, grid);
 }
 
 // ---- int8 weights, direct to LDS ----------------------------------------------
@@ -1744,7 +1762,7 @@ void launch_gemm_generic(const GemmGenericArgs& g, hipStream_t s) {
 
 enum GemmKind {
   K_GEMV, K_MFMA_256, K_MFMA_128, K_MFMA_64, K_MFMA_64x64, K_LDS_256, K_LDS_128, K_LDS_64x128, K_LDS_64x64,
-  K_LDS_256W8, K_LDS_128W8, K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64, K_F32, K_GENERIC_LINEAR
+  K_LDS_256W8, K_LDS_128W8, K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64, K_F32, K_GENERIC_LINEAR, K_LDS_SLIM
 };
 
 // Whether every 16-byte (or 8-byte, int8 GEMV) vector load a kernel makes
@@ -1821,12 +1839,20 @@ static GemmKind choose(const GemmArgs& a) {
       if (!strcmp(pin, "64x64lds") && a.w_dtype != NDX_I8) return K_LDS_64x64;
       if (!strcmp(pin, "256w8lds") && a.w_dtype != NDX_I8) return K_LDS_256W8;
       if (!strcmp(pin, "128w8lds") && a.w_dtype != NDX_I8) return K_LDS_128W8;
+      if (!strcmp(pin, "slim") && a.w_dtype != NDX_I8)
+        return a.K % BK == 0 && epi_fast_ok(a, 64) ? K_LDS_SLIM : K_LDS_64x64;
       if (a.w_dtype == NDX_I8 && a.qblock % 32 == 0) {
         if (!strcmp(pin, "256w8lds") || !strcmp(pin, "256lds")) return K_W8_256W8;
         if (!strcmp(pin, "128lds")) return K_W8_128;
         if (!strcmp(pin, "64x128lds")) return K_W8_64x128;
         if (!strcmp(pin, "64x64lds")) return K_W8_64x64;
       }
+    }
+    // Hint 5: the register-capped 64 x 64 tile for the second stream, where
+    // its conditions hold (16-bit weights, whole K tiles, the fast epilogue).
+    if (a.tile_hint == 5 && a.w_dtype != NDX_I8) {
+      if (a.K % BK == 0 && epi_fast_ok(a, 64)) return K_LDS_SLIM;
+      return K_LDS_64x64;
     }
     static const GemmKind lds[4] = {K_LDS_256W8, K_LDS_128, K_LDS_64x128, K_LDS_64x64};
     static const GemmKind w8[4] = {K_W8_256W8, K_W8_128, K_W8_64x128, K_W8_64x64};
@@ -1852,6 +1878,7 @@ const char* gemm_family(const GemmArgs& a) {
     case K_LDS_128: return "gemm_mfma_lds_128x128";
     case K_LDS_64x128: return "gemm_mfma_lds_64x128";
     case K_LDS_64x64: return "gemm_mfma_lds_64x64";
+    case K_LDS_SLIM: return "gemm_mfma_lds_64x64_slim";
     case K_LDS_256W8: return "gemm_mfma_lds_256x256w8";
     case K_LDS_128W8: return "gemm_mfma_lds_128x128w8";
     case K_W8_256W8: return "gemm_w8_lds_256x256w8";
@@ -2173,6 +2200,15 @@ void launch_gemm(const GemmArgs& a, hipStream_t s) {
     case K_LDS_128: launch_mfma_lds<128, 128, 64, 64>(a, s); break;
     case K_LDS_64x128: launch_mfma_lds<64, 128, 32, 64>(a, s); break;
     case K_LDS_64x64: launch_mfma_lds<64, 64, 32, 32>(a, s); break;
+    case K_LDS_SLIM: {
+      const int tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64), grid = (tiles + 7) / 8 * 8;
+      const GemmArgs none{};
+      if (a.a_dtype == NDX_BF16)
+        hipLaunchKernelGGL(gemm_slim_kernel<__bf16>, dim3(grid, a.batch), dim3(256), 0, s, a, none, grid);
+      else
+        hipLaunchKernelGGL(gemm_slim_kernel<_Float16>, dim3(grid, a.batch), dim3(256), 0, s, a, none, grid);
+      break;
+    }
     case K_LDS_256W8:
       if (a.epilogue == EPI_QK_NORM_ROPE && qkn_wide_ok(a, a.qk_cols)) launch_mfma_lds<256, 256, 64, 128>(a, s);
       else launch_mfma_lds<256, 256, 128, 64>(a, s);

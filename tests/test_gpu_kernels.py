@@ -136,6 +136,37 @@ def test_linear_every_kernel_variant(device, monkeypatch, tile, M, K, N):
     assert rel_err(out, oracle.gelu_tanh(oracle.linear(x, w, b))) <= BF16_TOL
 
 
+@pytest.mark.parametrize("epi", ["gelu_tanh", "gated", "none"])
+@pytest.mark.parametrize("M,K,N", [(600, 1024, 1024), (1024, 3072, 3072), (77, 320, 2048)])
+def test_linear_register_capped_tile(device, monkeypatch, epi, M, K, N):
+    """The 64 x 64 tile capped at 64 registers (the second stream's, so it
+    fits beside a 256 x 256 workgroup), pinned through NDX_GEMM_TILE=slim,
+    against the oracle: ragged M, whole K tiles, the fast epilogue's
+    activation, gated fp32 residual and plain forms."""
+    print(f"[gpu] register-capped tile {epi} M={M} K={K} N={N}", flush=True)
+    monkeypatch.setenv("NDX_GEMM_TILE", "slim")
+    x = bf(normal("sx", (1, 1, M, K)))
+    w = bf(normal("sw", (N, K), 0.02))
+    b = bf(normal("sb", (N,), 0.02))
+    res = normal("sr", (1, 1, M, N))
+    gate = normal("sg", (1, 1, 1, N))
+    model = nd.ModelBuilder(device, DT.BFloat16)
+    xin = model.Placeholder([1, 1, M, K])
+    rin = model.Placeholder([1, 1, M, N], DT.Float32)
+    gin = model.Placeholder([1, 1, 1, N], DT.Float32)
+    kw = {"gelu_tanh": {"activation": "gelu_tanh"}, "gated": {"gate": gin, "residual": rin}, "none": {}}[epi]
+    model.Compile([Layers.Linear(model, xin, HostTensor.FromFloats(w), HostTensor.FromFloats(b), **kw)])
+    model.Compiled.SetProfiling(True)
+    out = run(model, HostTensor.FromFloats(x).ConvertTo(DT.BFloat16), HostTensor.FromFloats(res),
+              HostTensor.FromFloats(gate))[0]
+    (family,) = set(model.Compiled.Profile())
+    model.Dispose()
+    assert family == "gemm_mfma_lds_64x64_slim", family
+    p = oracle.linear(x, w, b)
+    ref = {"gelu_tanh": lambda: oracle.gelu_tanh(p), "gated": lambda: res + gate * p, "none": lambda: p}[epi]()
+    assert rel_err(out, ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("epi", ["gelu_tanh", "gelu", "silu", "gated", "residual"])
 def test_linear_epilogues(device, epi):
     M, K, N = 300, 512, 384
