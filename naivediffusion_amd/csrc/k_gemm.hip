@@ -528,20 +528,27 @@ template <int TN, int WN, typename T, typename OT, int MODE>
 __device__ __forceinline__ void fast_slice(const GemmArgs& a, int64_t bidx, const EpiLane& L, f32x16 (&acc)[TN],
                                            float* stage, int row0) {
   constexpr int CS = WN + 4, C4 = WN / 4, RSTEP = 64 / C4, IT = 32 / RSTEP;
+  // Residual rows in flight at once: all of a slice's on 64-column waves (8),
+  // groups of 8 on 128-column ones (16 rows a slice would hold 64 more
+  // registers and spill).
+  constexpr int PF = IT < 8 ? IT : 8;
   constexpr int ES = (int)sizeof(OT);
   const int lane = threadIdx.x & 63, lrow = lane & 31, lhalf = lane >> 5;
   const __amdgpu_buffer_rsrc_t rc = make_rsrc((const OT*)a.c + bidx * a.batch_c, (uint32_t)(int64_t(a.M) * a.ldc * ES));
-  float4 res[MODE == FM_RESID ? IT : 1];
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(MODE == FM_RESID ? (const OT*)a.resid + bidx * a.batch_r : nullptr,
+                                              MODE == FM_RESID ? (uint32_t)(int64_t(a.M) * a.ldr * ES) : 0u);
+  float4 res[MODE == FM_RESID ? PF : 1];
   float rb[IT];
-  if constexpr (MODE == FM_RESID) {
-    const __amdgpu_buffer_rsrc_t rr =
-        make_rsrc((const OT*)a.resid + bidx * a.batch_r, (uint32_t)(int64_t(a.M) * a.ldr * ES));
+  auto load_res = [&](int h) __attribute__((always_inline)) {
+    if constexpr (MODE == FM_RESID) {
 #pragma unroll
-    for (int t = 0; t < IT; t++) {
-      const int row = row0 + L.rl0 + t * RSTEP;
-      res[t] = buf_load4<OT>(rr, uint32_t((row * a.ldr + L.col) * ES));
+      for (int t = 0; t < PF; t++) {
+        const int row = row0 + L.rl0 + (h + t) * RSTEP;
+        res[t] = buf_load4<OT>(rr, uint32_t((row * a.ldr + L.col) * ES));
+      }
     }
-  }
+  };
+  load_res(0);
   load_row_bias(a, row0 + L.rl0, RSTEP, rb);
 #pragma unroll
   for (int j = 0; j < TN; j++)
@@ -568,18 +575,24 @@ __device__ __forceinline__ void fast_slice(const GemmArgs& a, int64_t bidx, cons
     else act_rows([](float x) { return silu_f(x); });
   } else {
 #pragma unroll
-    for (int t = 0; t < IT; t++) {
-      const int rl = L.rl0 + t * RSTEP, row = row0 + rl;
-      const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
-      float x[4] = {v.x + L.bias.x + rb[t], v.y + L.bias.y + rb[t], v.z + L.bias.z + rb[t], v.w + L.bias.w + rb[t]};
-      if constexpr (MODE == FM_RESID) {
-        const float4 g = row >= a.gate_split ? L.gate2 : L.gate;
-        x[0] = res[t].x + g.x * (float)(T)x[0];
-        x[1] = res[t].y + g.y * (float)(T)x[1];
-        x[2] = res[t].z + g.z * (float)(T)x[2];
-        x[3] = res[t].w + g.w * (float)(T)x[3];
+    for (int h = 0; h < IT; h += PF) {
+      if (h > 0) load_res(h);
+#pragma unroll
+      for (int u = 0; u < PF; u++) {
+        const int t = h + u;
+        const int rl = L.rl0 + t * RSTEP, row = row0 + rl;
+        const float4 v = *(const float4*)&stage[rl * CS + L.c4 * 4];
+        float x[4] = {v.x + L.bias.x + rb[t], v.y + L.bias.y + rb[t], v.z + L.bias.z + rb[t],
+                      v.w + L.bias.w + rb[t]};
+        if constexpr (MODE == FM_RESID) {
+          const float4 g = row >= a.gate_split ? L.gate2 : L.gate;
+          x[0] = res[u].x + g.x * (float)(T)x[0];
+          x[1] = res[u].y + g.y * (float)(T)x[1];
+          x[2] = res[u].z + g.z * (float)(T)x[2];
+          x[3] = res[u].w + g.w * (float)(T)x[3];
+        }
+        buf_store4<OT>(rc, uint32_t((row * a.ldc + L.col) * ES), x);
       }
-      buf_store4<OT>(rc, uint32_t((row * a.ldc + L.col) * ES), x);
     }
   }
   wave_lds_sync();
