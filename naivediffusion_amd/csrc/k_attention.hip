@@ -67,15 +67,20 @@ struct AMfma<_Float16> {
   }
 };
 
+// Both segments' addresses are formed from fields read by constant index and
+// one of them selected: a per-lane choice of which field to read (an index
+// into the argument block) makes the compiler copy the block to scratch.
 template <typename T>
 __device__ __forceinline__ const T* seg_row(const AttnSeg& s, int64_t b, int64_t r) {
-  if (r < s.rows0) return (const T*)s.ptr[0] + b * s.batch[0] + r * s.ld[0];
-  return (const T*)s.ptr[1] + b * s.batch[1] + (r - s.rows0) * s.ld[1];
+  const T* first = (const T*)s.ptr[0] + b * s.batch[0] + r * s.ld[0];
+  const T* second = (const T*)s.ptr[1] + b * s.batch[1] + (r - s.rows0) * s.ld[1];
+  return r < s.rows0 ? first : second;
 }
 
 __device__ __forceinline__ void* out_row(const AttnArgs& a, int64_t b, int64_t r, int esize) {
-  if (r < a.out_rows0) return (char*)a.out[0] + (b * a.out_batch[0] + r * a.out_ld[0]) * esize;
-  return (char*)a.out[1] + (b * a.out_batch[1] + (r - a.out_rows0) * a.out_ld[1]) * esize;
+  char* first = (char*)a.out[0] + (b * a.out_batch[0] + r * a.out_ld[0]) * esize;
+  char* second = (char*)a.out[1] + (b * a.out_batch[1] + (r - a.out_rows0) * a.out_ld[1]) * esize;
+  return r < a.out_rows0 ? first : second;
 }
 
 // Decodes a workgroup id into (query block, head, batch), keeping each XCD on
@@ -512,11 +517,13 @@ __global__ __launch_bounds__(256) void flash_attn_f32_kernel(AttnArgs a, int gri
   const int qi = qb * BQ + wave * 32 + lq;
   const int qm = min(qi, a.T - 1);
 
-  float qf[DH];
+  // The query half-row as float4 values indexed by constants only (a float
+  // array written through float4 pointers would live in scratch memory).
+  float4 qf[DH / 4];
   {
     const float* qrow = seg_row<float>(a.q, b, qm) + col0 + lh * DH;
 #pragma unroll
-    for (int t = 0; t < DH; t += 4) *(float4*)&qf[t] = *(const float4*)(qrow + t);
+    for (int t = 0; t < DH / 4; t++) qf[t] = *(const float4*)(qrow + 4 * t);
   }
 
   float4 rk[F4], rv[F4];
@@ -571,14 +578,15 @@ __global__ __launch_bounds__(256) void flash_attn_f32_kernel(AttnArgs a, int gri
     for (int t = 0; t < DH; t += 4) {
       const float4 a0 = *(const float4*)(k0 + t);
       const float4 a1 = *(const float4*)(k1 + t);
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, qf[t], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, qf[t], sacc[1], 0, 0, 0);
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, qf[t + 1], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, qf[t + 1], sacc[1], 0, 0, 0);
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, qf[t + 2], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, qf[t + 2], sacc[1], 0, 0, 0);
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, qf[t + 3], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, qf[t + 3], sacc[1], 0, 0, 0);
+      const float4 q = qf[t / 4];
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, q.x, sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, q.x, sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, q.y, sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, q.y, sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, q.z, sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, q.z, sacc[1], 0, 0, 0);
+      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, q.w, sacc[0], 0, 0, 0);
+      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, q.w, sacc[1], 0, 0, 0);
     }
 
     const bool tail = (kb + 1) * BKEY > a.S;
