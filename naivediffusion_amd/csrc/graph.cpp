@@ -1680,6 +1680,25 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
   };
   for (int o : outs) mark_value(o);
 
+  // Whether value `owner` (and every view of it) is read by node `reader`
+  // alone among the scheduled nodes, and is no output.
+  const char* fuse_gn_env = getenv("NDX_FUSE_GN_NHWC");
+  const bool fuse_gn_nhwc = !(fuse_gn_env && fuse_gn_env[0] == '0');
+  auto sole_reader = [&](int owner, size_t reader) {
+    for (int o : outs)
+      if (c.values[o].base == owner) return false;
+    for (size_t k = 0; k < src.size(); k++) {
+      if (!need_node[k] || k == reader) continue;
+      const GNode& u = src[k];
+      std::vector<int> reads(u.in.begin(), u.in.end());
+      if (u.op == OP_ATTN)
+        for (int j = 0; j < 3; j++) reads.insert(reads.end(), {u.seg[j][0], u.seg[j][1]});
+      for (int id : reads)
+        if (id >= 0 && c.values[id].base == owner) return false;
+    }
+    return true;
+  };
+
   // Schedule in creation order, packing what a kernel cannot read as is.
   for (size_t i = 0; i < src.size(); i++) {
     if (!need_node[i]) continue;
@@ -1744,7 +1763,8 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
           if (id >= 0 && !c.values[c.values[id].base].quant) ensure_packed(id);
         const View4& xv = c.values[n.in[0]].v;
         const int64_t count = xv.size[1] / n.i0 * xv.size[2] * xv.size[3];
-        n.scratch_bytes = int64_t(xv.size[0]) * n.i0 * group_norm_splits(count) * 3 * sizeof(float);
+        // The split partials, then (mean, rstd) per (n, group) for the NHWC apply.
+        n.scratch_bytes = int64_t(xv.size[0]) * n.i0 * (group_norm_splits(count) * 3 + 2) * sizeof(float);
         break;
       }
       case OP_PATCH:
@@ -1768,9 +1788,29 @@ extern "C" NDX_API ndx_status ndx_graph_compile(ndx_graph* g, const ndx_value* o
         // reordered once.
         const GValue& x = c.values[n.in[0]];
         const View4& v = x.v;
-        const bool nhwc = x.offset % 8 == 0 && v.stride[1] == 1 && v.stride[3] == v.size[1] &&
+        bool nhwc = x.offset % 8 == 0 && v.stride[1] == 1 && v.stride[3] == v.size[1] &&
                           v.stride[2] == v.size[3] * v.size[1] &&
                           (v.size[0] == 1 || v.stride[0] == v.size[1] * v.size[2] * v.size[3]);
+        // A group norm read by this convolution alone writes NHWC itself
+        // (NDX_FUSE_GN_NHWC=0, read at compile time, keeps the copy).
+        if (!nhwc && fuse_gn_nhwc && x.kind == VK_NODE && x.base == n.in[0] && x.offset == 0 && is_packed(v) &&
+            x.producer >= 0 && src[x.producer].op == OP_GROUPNORM && sole_reader(n.in[0], i)) {
+          const GValue& gx = c.values[src[x.producer].in[0]];
+          if (group_norm_nhwc_ok(gx.dtype, x.dtype, v.size[1], v.size[2] * v.size[3], src[x.producer].i0) &&
+              gx.offset % 8 == 0 && is_packed(gx.v)) {
+            for (auto it = sched.rbegin(); it != sched.rend(); ++it)
+              if (it->op == OP_GROUPNORM && it->out == n.in[0]) {
+                it->i2 = 1;
+                View4& nv = c.values[n.in[0]].v;
+                nv.stride[1] = 1;
+                nv.stride[3] = nv.size[1];
+                nv.stride[2] = nv.size[3] * nv.size[1];
+                nv.stride[0] = nv.size[2] * nv.size[3] * nv.size[1];
+                nhwc = true;
+                break;
+              }
+          }
+        }
         if (!nhwc) {
           ensure_packed(n.in[0]);
           GNode t;
@@ -2308,6 +2348,7 @@ struct Runner {
         }
         a.partial = (float*)(arena + n.scratch_off);
         a.splits = group_norm_splits(int64_t(a.C / a.groups) * a.HW);
+        a.nhwc = n.i2;
         launch_group_norm(a, s);
         break;
       }

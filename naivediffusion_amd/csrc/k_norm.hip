@@ -5,6 +5,7 @@
 // and GroupNorm (+affine, +SiLU).
 
 #include <algorithm>
+#include <cstdlib>
 #include <stdexcept>
 
 #include "k_common.h"
@@ -1021,10 +1022,115 @@ __global__ __launch_bounds__(256) void group_norm_apply_kernel(GroupNormArgs a) 
   }
 }
 
+// Where group_norm_final_kernel leaves (mean, rstd) per (n, group): after the
+// split partials in the same scratch.
+__device__ __forceinline__ float* group_norm_final(const GroupNormArgs& a) {
+  return a.partial + int64_t(a.N) * a.groups * a.splits * 3;
+}
+
+// The statistics of each (n, group) combined from its split partials
+// (Chan's pairwise update, as group_norm_apply_kernel does per workgroup),
+// once: thread i of the grid takes (n, g) = (i / groups, i % groups).
+__global__ __launch_bounds__(64) void group_norm_final_kernel(GroupNormArgs a) {
+  const int i = blockIdx.x * 64 + threadIdx.x;
+  if (i >= a.N * a.groups) return;
+  const float* p = a.partial + int64_t(i) * a.splits * 3;
+  float c = 0.f, mean = 0.f, m2 = 0.f;
+  for (int k = 0; k < a.splits; k++) {
+    const float cb = p[3 * k], mb = p[3 * k + 1], qb = p[3 * k + 2];
+    if (cb == 0.f) continue;
+    const float ct = c + cb, d = mb - mean;
+    mean += d * (cb / ct);
+    m2 += qb + d * d * (c * cb / ct);
+    c = ct;
+  }
+  float* f = group_norm_final(a) + int64_t(i) * 2;
+  f[0] = mean;
+  f[1] = 1.0f / sqrtf(m2 / c + a.eps);
+}
+
+// The apply writing NHWC, the layout the implicit-GEMM convolution reads,
+// so no NCHW -> NHWC copy follows: a workgroup takes PT pixels of one image
+// and every channel. The per-group statistics are combined from the split
+// partials as group_norm_apply_kernel does; each channel's PT pixels are read
+// by PT / 8 lanes in 16-byte loads, normalised with the same arithmetic
+// (x * (weight * rstd) + (bias - mean * weight * rstd), then SiLU), staged
+// transposed in LDS, and written as whole NHWC pixel rows in 16-byte stores.
+// PT = 64 for up to 512 channels, 32 for up to 1280.
+template <typename T, int PT, int CMAX>
+__global__ __launch_bounds__(256) void group_norm_apply_nhwc_kernel(GroupNormArgs a) {
+  constexpr int LPC = PT / 8, CPP = 256 / LPC;  // lanes per channel, channels per pass
+  __shared__ float gstat[128];
+  __shared__ __attribute__((aligned(16))) T tile[PT * (CMAX + 8)];
+  const int LDC = a.C + 8;
+  const int n = blockIdx.y, p0 = blockIdx.x * PT, tid = threadIdx.x;
+  const int cpg = a.C / a.groups;
+  // (mean, rstd) of each group of image n, finalised once by
+  // group_norm_final_kernel after the split partials.
+  if (tid < 2 * a.groups) gstat[tid] = group_norm_final(a)[int64_t(n) * a.groups * 2 + tid];
+  __syncthreads();
+  const int pg = tid % LPC, cl = tid / LPC;
+  for (int c0 = 0; c0 < a.C; c0 += CPP) {
+    const int c = c0 + cl;
+    if (c < a.C) {
+      const int g = c / cpg;
+      const float mean = gstat[2 * g], rstd = gstat[2 * g + 1];
+      const float w = a.weight ? load_f(a.weight, a.w_dtype, c) * rstd : rstd;
+      const float b = (a.bias ? load_f(a.bias, a.w_dtype, c) : 0.f) - mean * w;
+      const uint4 u = *(const uint4*)((const T*)a.x + (int64_t(n) * a.C + c) * a.HW + p0 + pg * 8);
+      const T* xv = (const T*)&u;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float y = (float)xv[e] * w + b;
+        if (a.silu) y = silu_f(y);
+        tile[(pg * 8 + e) * LDC + c] = (T)y;
+      }
+    }
+  }
+  __syncthreads();
+  const int cw = a.C / 8;  // 16-byte chunks in a pixel row
+  for (int k = tid; k < PT * cw; k += 256) {
+    const int p = k / cw, cc = (k - p * cw) * 8;
+    *(uint4*)((T*)a.y + (int64_t(n) * a.HW + p0 + p) * a.C + cc) = *(const uint4*)&tile[p * LDC + cc];
+  }
+}
+
+// What the NHWC apply can take: 16-bit data, C a multiple of 8 up to 1280,
+// whole pixel tiles, at most 64 groups.
+static bool group_norm_nhwc_shape(int dtype, int y_dtype, int64_t C, int64_t HW, int groups) {
+  return dtype == y_dtype && (dtype == NDX_BF16 || dtype == NDX_F16) && C % 8 == 0 && C <= 1280 &&
+         HW % (C <= 512 ? 64 : 32) == 0 && groups <= 64;
+}
+
+// Where the graph writes a group norm's output NHWC: up to 512 channels. The
+// 32-pixel tiles of wider images cost more than the copy they remove (SDXL's
+// 640- and 1280-channel norms: 32.68 against 32.45 ms a step); they are
+// taken with NDX_GN_NHWC_WIDE=1 (read at compile time).
+bool group_norm_nhwc_ok(int dtype, int y_dtype, int64_t C, int64_t HW, int groups) {
+  const char* wide = getenv("NDX_GN_NHWC_WIDE");
+  return group_norm_nhwc_shape(dtype, y_dtype, C, HW, groups) && (C <= 512 || (wide && wide[0] == '1'));
+}
+
 void launch_group_norm(const GroupNormArgs& a, hipStream_t s) {
   dim3 g(a.N * a.groups, a.splits);
   hipLaunchKernelGGL(group_norm_stats_kernel, g, dim3(256), 0, s, a);
-  hipLaunchKernelGGL(group_norm_apply_kernel, g, dim3(256), 0, s, a);
+  if (!a.nhwc) {
+    hipLaunchKernelGGL(group_norm_apply_kernel, g, dim3(256), 0, s, a);
+    return;
+  }
+  if (!group_norm_nhwc_shape(a.dtype, a.y_dtype, a.C, a.HW, a.groups) || (uintptr_t)a.x % 16 || (uintptr_t)a.y % 16)
+    throw std::runtime_error("group norm: an NHWC output needs 16-bit data, C a multiple of 8 up to 1280 and whole "
+                             "pixel tiles");
+  hipLaunchKernelGGL(group_norm_final_kernel, dim3((a.N * a.groups + 63) / 64), dim3(64), 0, s, a);
+  const bool wide = a.C > 512;
+  dim3 gn(a.HW / (wide ? 32 : 64), a.N);
+  if (a.dtype == NDX_BF16) {
+    if (wide) hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<__bf16, 32, 1280>), gn, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<__bf16, 64, 512>), gn, dim3(256), 0, s, a);
+  } else {
+    if (wide) hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<_Float16, 32, 1280>), gn, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((group_norm_apply_nhwc_kernel<_Float16, 64, 512>), gn, dim3(256), 0, s, a);
+  }
 }
 
 // Softmax over the last axis (DmlOps.ActivationSoftmax with axes {3},

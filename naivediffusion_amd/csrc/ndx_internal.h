@@ -195,7 +195,12 @@ struct GroupNormArgs {
   // Split statistics: `splits` workgroups per (n, group) each leave (count,
   // mean, M2) in `partial` (N * groups * splits * 3 floats of scratch).
   float* partial; int splits;
+  // The output in NHWC ([N, H, W, C] packed), for the implicit-GEMM
+  // convolution that reads it (group_norm_nhwc_ok).
+  int nhwc;
 };
+// Whether the group norm can write NHWC for this shape and type.
+bool group_norm_nhwc_ok(int dtype, int y_dtype, int64_t C, int64_t HW, int groups);
 // The split count the group norm uses for a shape, and its scratch bytes.
 int group_norm_splits(int64_t count);
 

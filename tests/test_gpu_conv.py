@@ -183,3 +183,37 @@ def test_conv_direct_path(device, case):
         wq = (q.astype(np.float32).reshape(rows, -1, 32) * oracle.f16_bits_to_f32(sc)[:, :, None]).reshape(w.shape)
     assert not any(f.startswith("conv_mfma_") for f in families), families
     assert rel_err(out, oracle.conv2d(x, wq, b, 1, 1)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype,B,C,H,W,Cout", [(DT.BFloat16, 1, 128, 16, 16, 128), (DT.Float16, 2, 320, 8, 16, 64),
+                                                (DT.Float16, 2, 640, 8, 12, 96)])
+def test_group_norm_writes_the_convolutions_nhwc_input(device, monkeypatch, dtype, B, C, H, W, Cout):
+    """GroupNorm(32) + SiLU read by a convolution alone writes the NHWC image
+    the implicit GEMM reads (no transposed copy; 64-pixel tiles up to 512
+    channels, 32-pixel ones above, taken with NDX_GN_NHWC_WIDE=1): bit for
+    bit what the NCHW norm and the
+    copy give (NDX_FUSE_GN_NHWC=0), and within the tolerance of the oracle's
+    group norm and convolution (UNetLayers.cs:14-47, Graph/Layers.cs:166-185)."""
+    print(f"[gpu] group norm into conv {dtype.name} {B}x{C}x{H}x{W} -> {Cout}", flush=True)
+    if C > 512:
+        monkeypatch.setenv("NDX_GN_NHWC_WIDE", "1")
+    x = narrow(normal("gnc_x", (B, C, H, W)), dtype)
+    gw = narrow(normal("gnc_gw", (C,), 0.2) + 1.0, dtype)
+    gb = narrow(normal("gnc_gb", (C,), 0.2), dtype)
+    w = narrow(normal("gnc_w", (Cout, C, 3, 3), 1.0 / np.sqrt(C * 9)), dtype)
+    b = narrow(normal("gnc_b", (Cout,), 0.1), dtype)
+
+    def build(m, xi):
+        h = Layers.GroupNorm(m, xi, HostTensor.FromFloats(gw), HostTensor.FromFloats(gb), 32, 1e-5, silu=True)
+        return Layers.Conv2d(m, h, HostTensor.FromFloats(w), HostTensor.FromFloats(b), 1, 1)
+
+    fused, families = run_graph(device, dtype, build, x)
+    assert "nchw_to_nhwc" not in families, families
+    monkeypatch.setenv("NDX_FUSE_GN_NHWC", "0")
+    plain, plain_families = run_graph(device, dtype, build, x)
+    assert "nchw_to_nhwc" in plain_families, plain_families
+    assert np.array_equal(fused, plain)
+    h = narrow(oracle.group_norm(x, 32, gw, gb, 1e-5, silu=True), dtype)
+    err = rel_err(fused, oracle.conv2d(h, w, b, 1, 1))
+    print(f"[gpu]   rel err {err:.2e}", flush=True)
+    assert err <= TOL[dtype]
